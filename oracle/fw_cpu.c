@@ -1,0 +1,556 @@
+/*
+ * fw_cpu — CPU restatement of forword.c's forward.  TEST INFRASTRUCTURE:
+ * only the tests, the smoke check and the benchmark's CPU-baseline leg use it.
+ *
+ * Build with contraction off (-ffp-contract=off): every a*b+c below that is not
+ * an explicit fmaf() must round twice, as in the reference's ISO-C build.
+ * Each function cites the reference code whose operation order it follows.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "fw_cpu.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ── scalar helpers ──────────────────────────────────────────────────────── */
+
+/* half_to_float (quant_matvec.c:22-50): exact, subnormals normalised by shifting. */
+float fwc_half_to_float(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t ex = (h >> 10) & 31u, mant = h & 1023u, bits;
+    if (ex == 0) {
+        if (mant == 0) bits = sign;
+        else {
+            int e = -14;
+            while (!(mant & 1024u)) { mant <<= 1; --e; }
+            bits = sign | ((uint32_t)(e + 127) << 23) | ((mant & 1023u) << 13);
+        }
+    } else if (ex == 31) bits = sign | 0x7f800000u | (mant << 13);
+    else bits = sign | ((ex + 112u) << 23) | (mant << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void fwc_half_to_float_n(const uint16_t *h, float *out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = fwc_half_to_float(h[i]);
+}
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/*
+ * simd_dot_f32, AVX2+FMA branch (simd.h:27-67) plus the scalar tail
+ * (simd.h:151-153): two 8-lane FMA accumulators over 16-wide steps, merged,
+ * one more 8-lane FMA step per remaining 8, then the horizontal tree
+ * (lo128+hi128, movehl, shuffle) and `0.0f + tree`.
+ */
+float fwc_dot_f32(const float *a, const float *b, size_t n)
+{
+    size_t i = 0;
+    float sum = 0.0f, acc0[8] = { 0 }, acc1[8] = { 0 };
+    for (; i + 16 <= n; i += 16) {
+        for (int l = 0; l < 8; l++) acc0[l] = fmaf(a[i + l], b[i + l], acc0[l]);
+        for (int l = 0; l < 8; l++) acc1[l] = fmaf(a[i + 8 + l], b[i + 8 + l], acc1[l]);
+    }
+    for (int l = 0; l < 8; l++) acc0[l] = acc0[l] + acc1[l];
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) acc0[l] = fmaf(a[i + l], b[i + l], acc0[l]);
+    float s0 = acc0[0] + acc0[4], s1 = acc0[1] + acc0[5], s2 = acc0[2] + acc0[6], s3 = acc0[3] + acc0[7];
+    float r = (s0 + s2) + (s1 + s3);
+    sum += r;
+    for (; i < n; i++) sum += a[i] * b[i];
+    return sum;
+}
+
+/* dot_q8_0_block, AVX2+FMA branch (quant_matvec.c:65-114). */
+static float dot_q8_0(const uint8_t *p, const float *x)
+{
+    float d = fwc_half_to_float(rd16(p));
+    const int8_t *qs = (const int8_t *)(p + 2);
+    float prod[32], s[8];
+    for (int j = 0; j < 32; j++) prod[j] = fmaf((float)qs[j], x[j], 0.0f);
+    for (int l = 0; l < 8; l++) s[l] = (prod[l] + prod[8 + l]) + (prod[16 + l] + prod[24 + l]);
+    float t0 = s[0] + s[4], t1 = s[1] + s[5], t2 = s[2] + s[6], t3 = s[3] + s[7];
+    return d * ((t0 + t2) + (t1 + t3));
+}
+
+/* Q5_0 block decode (decode_small_block, quant_matvec.c:197-213; linear.c:40-56). */
+static void decode_q5_0(const uint8_t *p, float *w)
+{
+    float d = fwc_half_to_float(rd16(p));
+    const uint8_t *qh = p + 2, *qs = p + 6;
+    for (int j = 0; j < 16; j++) {
+        int h0 = (qh[j / 8] >> (j % 8)) & 1;
+        int h1 = (qh[(j + 16) / 8] >> ((j + 16) % 8)) & 1;
+        int q0 = (qs[j] & 15) | (h0 << 4), q1 = (qs[j] >> 4) | (h1 << 4);
+        w[j] = d * (float)(q0 - 16);
+        w[j + 16] = d * (float)(q1 - 16);
+    }
+}
+
+/*
+ * Q4_0 block decode.  Not in the reference (quant_matvec.c:52-62 has no case);
+ * written from the GGUF block definition in the shape of the reference's other
+ * 32-value decoder: w_j = d*(float)(q_j-8), q_j = qs[j]&15, q_{j+16} = qs[j]>>4.
+ */
+static void decode_q4_0(const uint8_t *p, float *w)
+{
+    float d = fwc_half_to_float(rd16(p));
+    const uint8_t *qs = p + 2;
+    for (int j = 0; j < 16; j++) {
+        w[j] = d * (float)((qs[j] & 15) - 8);
+        w[j + 16] = d * (float)((qs[j] >> 4) - 8);
+    }
+}
+
+/* q8_0_decode inner loop (quant.c:254-259). */
+static void decode_q8_0(const uint8_t *p, float *w)
+{
+    float d = fwc_half_to_float(rd16(p));
+    const int8_t *qs = (const int8_t *)(p + 2);
+    for (int j = 0; j < 32; j++) w[j] = d * (float)qs[j];
+}
+
+static size_t block_bytes(uint32_t t)
+{
+    switch (t) {
+    case FORWORD_GGML_Q4_0: return 18;
+    case FORWORD_GGML_Q5_0: return 22;
+    case FORWORD_GGML_Q8_0: return 34;
+    default: return 0;
+    }
+}
+
+int fwc_dequant(const void *blocks, size_t bytes, uint32_t type, float *out, size_t count)
+{
+    size_t bb = block_bytes(type);
+    if (!blocks || !out || !bb || !bytes || bytes % bb || count % 32 || bytes / bb != count / 32)
+        return -1;
+    const uint8_t *p = (const uint8_t *)blocks;
+    for (size_t b = 0; b < bytes / bb; b++, p += bb) {
+        if (type == FORWORD_GGML_Q8_0) decode_q8_0(p, out + 32 * b);
+        else if (type == FORWORD_GGML_Q5_0) decode_q5_0(p, out + 32 * b);
+        else decode_q4_0(p, out + 32 * b);
+    }
+    return 0;
+}
+
+/* dot_quant_block (quant_matvec.c:231-261), with Q4_0 taking the Q5_0 route. */
+static float dot_block(const uint8_t *p, uint32_t type, const float *x)
+{
+    float w[32];
+    if (type == FORWORD_GGML_Q8_0) return dot_q8_0(p, x);
+    if (type == FORWORD_GGML_Q5_0) decode_q5_0(p, w);
+    else decode_q4_0(p, w);
+    return fwc_dot_f32(w, x, 32);
+}
+
+/* ── row-parallel driver ─────────────────────────────────────────────────── */
+
+static int g_threads = 1;
+void fwc_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 256 ? 256 : n); }
+
+typedef struct {
+    void (*fn)(void *ctx, size_t r0, size_t r1);
+    void *ctx;
+    size_t r0, r1;
+} span_t;
+
+static void *span_run(void *a)
+{
+    span_t *s = (span_t *)a;
+    s->fn(s->ctx, s->r0, s->r1);
+    return NULL;
+}
+
+/* fn over rows [0, n) split into contiguous spans; each row's arithmetic is
+ * independent of the split, so results are identical for any thread count. */
+static void par_rows_min(void (*fn)(void *, size_t, size_t), void *ctx, size_t n, size_t min_rows)
+{
+    int nt = g_threads;
+    if (nt > 1 && n >= min_rows) {
+        if ((size_t)nt > n) nt = (int)n;
+        span_t sp[256];
+        pthread_t tid[256];
+        int ok[256];
+        for (int i = 0; i < nt; i++) {
+            sp[i].fn = fn; sp[i].ctx = ctx;
+            sp[i].r0 = n * (size_t)i / (size_t)nt;
+            sp[i].r1 = n * (size_t)(i + 1) / (size_t)nt;
+            ok[i] = i > 0 && pthread_create(&tid[i], NULL, span_run, &sp[i]) == 0;
+        }
+        span_run(&sp[0]);
+        for (int i = 1; i < nt; i++) {
+            if (ok[i]) pthread_join(tid[i], NULL);
+            else span_run(&sp[i]);
+        }
+        return;
+    }
+    fn(ctx, 0, n);
+}
+
+static void par_rows(void (*fn)(void *, size_t, size_t), void *ctx, size_t n)
+{
+    par_rows_min(fn, ctx, n, 64);
+}
+
+typedef struct {
+    const uint8_t *w;
+    uint32_t type;
+    const float *x;
+    float *y;
+    size_t in, bpr, bb;
+} qmv_t;
+
+/* quant_matvec row loop (quant_matvec.c:293-309): sequential float sum over blocks. */
+static void qmv_rows(void *c, size_t r0, size_t r1)
+{
+    qmv_t *m = (qmv_t *)c;
+    for (size_t r = r0; r < r1; r++) {
+        const uint8_t *row = m->w + r * m->bpr * m->bb;
+        float sum = 0.0f;
+        for (size_t b = 0; b < m->bpr; b++) sum += dot_block(row + b * m->bb, m->type, m->x + 32 * b);
+        m->y[r] = sum;
+    }
+}
+
+static void f32mv_rows(void *c, size_t r0, size_t r1)
+{
+    qmv_t *m = (qmv_t *)c;
+    const float *w = (const float *)m->w;
+    for (size_t r = r0; r < r1; r++) m->y[r] = fwc_dot_f32(w + r * m->in, m->x, m->in);
+}
+
+/* quant_matvec (quant_matvec.c:263-312) incl. its argument checks (:274-289);
+ * type F32 takes linear_forward's F32 branch (linear.c:173-179). */
+int fwc_quant_matvec(const void *w, size_t w_size, uint32_t type, const float *x, float *y,
+                     size_t in, size_t out)
+{
+    if (!w || !x || !y || !in || !out) return -1;
+    qmv_t m = { (const uint8_t *)w, type, x, y, in, 0, 0 };
+    if (type == FORWORD_GGML_F32) {
+        if (out > SIZE_MAX / in / 4 || w_size < out * in * 4) return -1;
+        par_rows(f32mv_rows, &m, out);
+        return 0;
+    }
+    m.bb = block_bytes(type);
+    if (!m.bb || in % 32) return -1;
+    m.bpr = in / 32;
+    size_t rb = m.bpr * m.bb;
+    if (out > SIZE_MAX / rb || w_size < out * rb) return -1;
+    par_rows(qmv_rows, &m, out);
+    return 0;
+}
+
+int fwc_tensor_matvec_f32(const float *w, const float *x, float *y, size_t rows, size_t cols)
+{
+    if (!w || !x || !y || !rows || !cols) return -1;          /* tensor_ops.c:8-23 */
+    for (size_t r = 0; r < rows; r++) y[r] = fwc_dot_f32(w + r * cols, x, cols);
+    return 0;
+}
+
+/* rms_norm (norm.c:7-16): simd_sum_squares, then simd_mul and simd_scale. */
+void fwc_rms_norm(const float *x, const float *w, float *out, size_t n, float eps)
+{
+    float ss = fwc_dot_f32(x, x, n);
+    float scale = 1.0f / sqrtf((ss / (float)n) + eps);
+    if (w) {
+        for (size_t i = 0; i < n; i++) out[i] = x[i] * w[i];
+        for (size_t i = 0; i < n; i++) out[i] = out[i] * scale;
+    } else {
+        for (size_t i = 0; i < n; i++) out[i] = x[i] * scale;
+    }
+}
+
+/* rope_apply (rope.c:28-53). */
+void fwc_rope_apply(float *qk, size_t pos, size_t n_heads, size_t hd, const float *cos_tab,
+                    const float *sin_tab, int neox)
+{
+    size_t half = hd / 2;
+    const float *c = cos_tab + pos * half, *s = sin_tab + pos * half;
+    for (size_t h = 0; h < n_heads; h++) {
+        float *v = qk + h * hd;
+        for (size_t i = 0; i < half; i++) {
+            size_t i0 = neox ? i : 2 * i, i1 = neox ? half + i : 2 * i + 1;
+            float v0 = v[i0], v1 = v[i1];
+            v[i0] = v0 * c[i] - v1 * s[i];
+            v[i1] = v0 * s[i] + v1 * c[i];
+        }
+    }
+}
+
+/* softmax (attention.c:18-33): left unnormalised when the sum is <= 0 or not finite. */
+void fwc_softmax(float *x, size_t n)
+{
+    if (!n) return;
+    float mx = x[0];
+    for (size_t i = 1; i < n; i++) if (x[i] > mx) mx = x[i];
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) { x[i] = expf(x[i] - mx); sum += x[i]; }
+    if (sum <= 0.0f || !isfinite(sum)) return;
+    float inv = 1.0f / sum;
+    for (size_t i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* apply_silu (ffn.c:17-25) = tensor_silu (tensor_ops.c:63-81). */
+void fwc_silu(float *x, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i];
+        float sig = v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
+        x[i] = v * sig;
+    }
+}
+
+/* sampler_argmax (sampler.c:28-32). */
+uint32_t fwc_argmax(const float *x, size_t n)
+{
+    size_t best = 0;
+    for (size_t i = 1; i < n; i++) if (x[i] > x[best]) best = i;
+    return (uint32_t)best;
+}
+
+typedef struct {
+    const float *q, *kc, *vc;
+    float *out, *scores;        /* scores: [n_head][pos+1] scratch */
+    size_t n_head, n_kv, hd, pos;
+} attn_t;
+
+/* per-head body of attention_forward (attention.c:142-164), incl. simd_axpy_f32
+ * (simd.h:262-275: 8-wide FMA part, then a rounded multiply-add tail). */
+static void attn_heads(void *c, size_t h0, size_t h1)
+{
+    attn_t *a = (attn_t *)c;
+    const size_t group = a->n_head / a->n_kv, stride = a->n_kv * a->hd;
+    const float scale = 1.0f / sqrtf((float)a->hd);
+    for (size_t h = h0; h < h1; h++) {
+        size_t kvh = h / group;
+        const float *qh = a->q + h * a->hd;
+        float *oh = a->out + h * a->hd, *sc = a->scores + h * (a->pos + 1);
+        for (size_t t = 0; t <= a->pos; t++) {
+            float dot = fwc_dot_f32(qh, a->kc + t * stride + kvh * a->hd, a->hd);
+            sc[t] = dot * scale;
+        }
+        fwc_softmax(sc, a->pos + 1);
+        memset(oh, 0, a->hd * sizeof(float));
+        for (size_t t = 0; t <= a->pos; t++) {
+            const float *vt = a->vc + t * stride + kvh * a->hd;
+            float w = sc[t];
+            size_t i = 0;
+            for (; i + 8 <= a->hd; i += 8)
+                for (int l = 0; l < 8; l++) oh[i + l] = fmaf(vt[i + l], w, oh[i + l]);
+            for (; i < a->hd; i++) oh[i] += vt[i] * w;
+        }
+    }
+}
+
+void fwc_attention_core(const float *q, const float *kc, const float *vc, float *out, size_t n_head,
+                        size_t n_kv, size_t hd, size_t pos, float *scores)
+{
+    attn_t a = { q, kc, vc, out, scores, n_head, n_kv, hd, pos };
+    /* split heads across threads only when the work is large */
+    par_rows_min(attn_heads, &a, n_head, pos >= 1024 ? 2 : SIZE_MAX);
+}
+
+/* ── model ───────────────────────────────────────────────────────────────── */
+
+typedef struct {
+    const uint8_t *p;
+    uint32_t type;
+    size_t in, out, bytes;
+} lin_t;
+
+struct fwc_model {
+    forword_gpu_config_t c;
+    size_t n_ctx;
+    const uint8_t *data;
+    size_t data_size;
+    lin_t embd, out_w;
+    const float *out_norm;
+    struct layer {
+        const float *attn_norm, *ffn_norm;
+        lin_t q, k, v, o, gate, up, down;
+    } *L;
+    const float *cos_tab, *sin_tab;
+    float *kv_k, *kv_v;
+    float *x, *xn, *attn_out, *ffn_out, *q, *k, *v, *att, *gate, *upb, *scores, *logits, *trace;
+    int traced;
+};
+
+static const forword_gpu_tensor_t *find(const forword_gpu_tensor_t *t, size_t n, const char *name)
+{
+    for (size_t i = 0; i < n; i++) if (t[i].name && !strcmp(t[i].name, name)) return &t[i];
+    return NULL;
+}
+
+static int bind_lin(lin_t *l, const fwc_model_t *m, const forword_gpu_tensor_t *t)
+{
+    if (!t || t->n_dims < 2 || t->offset > m->data_size || t->byte_size > m->data_size - t->offset) return -1;
+    l->p = m->data + t->offset;
+    l->type = t->ggml_type;
+    l->in = (size_t)t->dims[0];
+    l->out = (size_t)t->dims[1];
+    l->bytes = (size_t)t->byte_size;
+    return 0;
+}
+
+static const float *bind_vec(const fwc_model_t *m, const forword_gpu_tensor_t *t, size_t n)
+{
+    if (!t || t->ggml_type != FORWORD_GGML_F32 || t->byte_size < n * 4 || t->offset > m->data_size ||
+        t->byte_size > m->data_size - t->offset) return NULL;
+    return (const float *)(m->data + t->offset);
+}
+
+void fwc_model_free(fwc_model_t *m)
+{
+    if (!m) return;
+    free(m->L); free(m->kv_k); free(m->kv_v); free(m->x); free(m->xn); free(m->attn_out);
+    free(m->ffn_out); free(m->q); free(m->k); free(m->v); free(m->att); free(m->gate); free(m->upb);
+    free(m->scores); free(m->logits); free(m->trace);
+    free(m);
+}
+
+fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gpu_tensor_t *t,
+                            size_t nt, const forword_gpu_config_t *cfg, size_t max_ctx,
+                            const float *cos_tab, const float *sin_tab)
+{
+    if (!data || !t || !cfg || !max_ctx || !cos_tab || !sin_tab) return NULL;
+    const forword_gpu_config_t *c = cfg;
+    if (c->norm_type != FORWORD_NORM_RMS || !c->use_ffn_gate || c->act_type != FORWORD_ACT_SILU ||
+        c->use_qkv_bias || c->parallel_res || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
+        c->n_head % c->n_head_kv || c->head_dim % 2 || c->n_embd != c->n_head * c->head_dim) {
+        fprintf(stderr, "fwc_model_init: unsupported model variant\n");
+        return NULL;
+    }
+    fwc_model_t *m = (fwc_model_t *)calloc(1, sizeof(*m));
+    if (!m) return NULL;
+    m->c = *c;
+    m->n_ctx = max_ctx;
+    m->data = (const uint8_t *)data;
+    m->data_size = data_size;
+    m->cos_tab = cos_tab;
+    m->sin_tab = sin_tab;
+    const forword_gpu_tensor_t *e = find(t, nt, "token_embd.weight");
+    const forword_gpu_tensor_t *o = find(t, nt, "output.weight");
+    if (!o) o = find(t, nt, "lm_head.weight");
+    if (!o) o = e;
+    if (bind_lin(&m->embd, m, e) || bind_lin(&m->out_w, m, o)) goto fail;
+    m->out_norm = bind_vec(m, find(t, nt, "output_norm.weight"), c->n_embd);
+    m->L = calloc(c->n_layer, sizeof(*m->L));
+    if (!m->L) goto fail;
+    for (uint32_t l = 0; l < c->n_layer; l++) {
+        char nm[96];
+        struct layer *L = &m->L[l];
+#define LIN(field, suffix) snprintf(nm, sizeof nm, "blk.%u." suffix, l); \
+        if (bind_lin(&L->field, m, find(t, nt, nm))) goto fail;
+        LIN(q, "attn_q.weight"); LIN(k, "attn_k.weight"); LIN(v, "attn_v.weight");
+        LIN(o, "attn_output.weight"); LIN(gate, "ffn_gate.weight"); LIN(up, "ffn_up.weight");
+        LIN(down, "ffn_down.weight");
+#undef LIN
+        snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l);
+        L->attn_norm = bind_vec(m, find(t, nt, nm), c->n_embd);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);
+        L->ffn_norm = bind_vec(m, find(t, nt, nm), c->n_embd);
+    }
+    size_t kvd = (size_t)c->n_head_kv * c->head_dim, kvn = (size_t)c->n_layer * max_ctx * kvd;
+    m->kv_k = calloc(kvn, 4); m->kv_v = calloc(kvn, 4);
+    m->x = calloc(c->n_embd, 4); m->xn = calloc(c->n_embd, 4); m->attn_out = calloc(c->n_embd, 4);
+    m->ffn_out = calloc(c->n_embd, 4); m->q = calloc(c->n_embd, 4); m->k = calloc(kvd, 4);
+    m->v = calloc(kvd, 4); m->att = calloc(c->n_embd, 4); m->gate = calloc(c->n_ff, 4);
+    m->upb = calloc(c->n_ff, 4); m->scores = calloc((size_t)c->n_head * max_ctx, 4);
+    m->logits = calloc(c->n_vocab, 4); m->trace = calloc((size_t)2 * c->n_layer * c->n_embd, 4);
+    if (!m->kv_k || !m->kv_v || !m->x || !m->xn || !m->attn_out || !m->ffn_out || !m->q || !m->k ||
+        !m->v || !m->att || !m->gate || !m->upb || !m->scores || !m->logits || !m->trace) goto fail;
+    return m;
+fail:
+    fprintf(stderr, "fwc_model_init: missing tensor or out of memory\n");
+    fwc_model_free(m);
+    return NULL;
+}
+
+static int lin(const lin_t *l, const float *x, float *y)
+{
+    return fwc_quant_matvec(l->p, l->bytes, l->type, x, y, l->in, l->out);
+}
+
+/* linear_get_row (linear.c:60-151) for F32/Q8_0/Q5_0; Q4_0 by its definition. */
+static int get_row(const lin_t *l, size_t row, float *out)
+{
+    if (row >= l->out) return -1;
+    if (l->type == FORWORD_GGML_F32) { memcpy(out, l->p + row * l->in * 4, l->in * 4); return 0; }
+    size_t bb = block_bytes(l->type);
+    if (!bb || l->in % 32) return -1;
+    size_t rb = l->in / 32 * bb;
+    return fwc_dequant(l->p + row * rb, rb, l->type, out, l->in);
+}
+
+float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
+{
+    const forword_gpu_config_t *c = &m->c;
+    const size_t n = c->n_embd, hd = c->head_dim, kvd = (size_t)c->n_head_kv * hd;
+    if (pos >= m->n_ctx || token >= c->n_vocab) return NULL;     /* transformer.c:156-164 */
+    if (get_row(&m->embd, token, m->x)) return NULL;             /* transformer.c:167-177 */
+    if (c->embd_scale != 1.0f) for (size_t i = 0; i < n; i++) m->x[i] *= c->embd_scale;
+    int neox = c->rope_type == FORWORD_ROPE_NEOX;
+    for (uint32_t l = 0; l < c->n_layer; l++) {                  /* transformer.c:255-289 */
+        struct layer *L = &m->L[l];
+        fwc_rms_norm(m->x, L->attn_norm, m->xn, n, c->norm_eps);
+        /* attention_forward (attention.c:124-166) */
+        if (lin(&L->q, m->xn, m->q) || lin(&L->k, m->xn, m->k) || lin(&L->v, m->xn, m->v)) return NULL;
+        fwc_rope_apply(m->q, pos, c->n_head, hd, m->cos_tab, m->sin_tab, neox);
+        fwc_rope_apply(m->k, pos, c->n_head_kv, hd, m->cos_tab, m->sin_tab, neox);
+        memcpy(fwc_kv_k(m, l, pos), m->k, kvd * 4);
+        memcpy(fwc_kv_v(m, l, pos), m->v, kvd * 4);
+        fwc_attention_core(m->q, fwc_kv_k(m, l, 0), fwc_kv_v(m, l, 0), m->att, c->n_head,
+                           c->n_head_kv, hd, pos, m->scores);
+        if (lin(&L->o, m->att, m->attn_out)) return NULL;
+        for (size_t i = 0; i < n; i++) m->x[i] += m->attn_out[i];
+        memcpy(m->trace + (2 * (size_t)l) * n, m->x, n * 4);
+        fwc_rms_norm(m->x, L->ffn_norm, m->xn, n, c->norm_eps);
+        /* ffn_forward gated branch (ffn.c:68-107) */
+        if (lin(&L->gate, m->xn, m->gate) || lin(&L->up, m->xn, m->upb)) return NULL;
+        fwc_silu(m->gate, c->n_ff);
+        for (size_t i = 0; i < c->n_ff; i++) m->gate[i] *= m->upb[i];
+        if (lin(&L->down, m->gate, m->ffn_out)) return NULL;
+        for (size_t i = 0; i < n; i++) m->x[i] += m->ffn_out[i];
+        memcpy(m->trace + (2 * (size_t)l + 1) * n, m->x, n * 4);
+    }
+    if (m->out_norm) fwc_rms_norm(m->x, m->out_norm, m->xn, n, c->norm_eps);   /* transformer.c:293-307 */
+    else memcpy(m->xn, m->x, n * 4);
+    if (lin(&m->out_w, m->xn, m->logits)) return NULL;          /* transformer.c:310-323 */
+    m->traced = 1;
+    return m->logits;
+}
+
+const float *fwc_trace(const fwc_model_t *m) { return m && m->traced ? m->trace : NULL; }
+
+float *fwc_kv_k(fwc_model_t *m, size_t layer, size_t pos)
+{
+    size_t kvd = (size_t)m->c.n_head_kv * m->c.head_dim;
+    return m->kv_k + (layer * m->n_ctx + pos) * kvd;              /* kv_cache.h:45-47 */
+}
+
+float *fwc_kv_v(fwc_model_t *m, size_t layer, size_t pos)
+{
+    size_t kvd = (size_t)m->c.n_head_kv * m->c.head_dim;
+    return m->kv_v + (layer * m->n_ctx + pos) * kvd;
+}
+
+int fwc_generate_greedy(fwc_model_t *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                        uint32_t *out_ids)
+{
+    if (!m || !prompt || !n_prompt || !out_ids) return -1;
+    float *lg = NULL;
+    for (size_t i = 0; i < n_prompt; i++)                        /* main.c:145-151 */
+        if (!(lg = fwc_forward(m, prompt[i], i))) return -1;
+    for (size_t g = 0; g < n_gen; g++) {                          /* main.c:173-217 */
+        out_ids[g] = fwc_argmax(lg, m->c.n_vocab);
+        if (g + 1 < n_gen && !(lg = fwc_forward(m, out_ids[g], n_prompt + g))) return -1;
+    }
+    return 0;
+}

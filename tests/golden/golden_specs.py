@@ -1,0 +1,135 @@
+"""Inputs of the golden fixtures: seeds, shapes and generators shared by
+tests/golden/make_golden.py (which records the reference's outputs) and the
+tests (which regenerate the same inputs and compare)."""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, os.path.join(ROOT, "forword.c_amd"))
+import fwgpu  # noqa: E402
+
+Q4, Q5, Q8 = fwgpu.GGML_Q4_0, fwgpu.GGML_Q5_0, fwgpu.GGML_Q8_0
+
+# Model fixtures.  "tiny": dim 288, ffn 768, 6 layers, 6/6 heads, vocab 32000,
+# ctx 256, all Q8_0, theta 1e4, 16-token prompt + 128 greedy tokens.  "gqa":
+# 8 query / 2 KV heads (group 4).  "q5": Q5_0 linears, embedding and output.
+MODELS = {
+    "tiny": {"spec": lambda: fwgpu.spec_tiny(seed=20240601), "n_prompt": 16, "n_gen": 128,
+             "max_ctx": 0, "prompt_seed": 1},
+    "gqa": {"spec": lambda: fwgpu.spec(256, 512, 2, 8, 2, 1000, 64, 10000.0, seed=77),
+            "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 2},
+    "q5": {"spec": lambda: fwgpu.spec(288, 768, 2, 6, 6, 4096, 64, 10000.0, linear_type=Q5,
+                                      embd_type=Q5, output_type=Q5, seed=55),
+           "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 3},
+}
+
+
+def prompt(name) -> np.ndarray:
+    m = MODELS[name]
+    vocab = m["spec"]().n_vocab
+    return np.random.default_rng(m["prompt_seed"]).integers(3, vocab, m["n_prompt"]).astype(np.uint32)
+
+
+def n_forwards(name) -> int:
+    return MODELS[name]["n_prompt"] + MODELS[name]["n_gen"] - 1
+
+
+def logit_steps(name):
+    n = n_forwards(name)
+    return [0, MODELS[name]["n_prompt"] - 1, n - 1]
+
+
+def trace_steps(name):
+    return [0, n_forwards(name) - 1]
+
+
+# quant_matvec fixtures: (type, rows=out, cols=in) at the microbenchmark shapes
+MATVEC_CASES = [(t, r, c) for t in (Q8, Q5) for (r, c) in ((4096, 4096), (14336, 4096), (4096, 14336))]
+
+
+def matvec_key(t, rows, cols):
+    return f"y_{fwgpu.TYPE_NAMES[t]}_{rows}x{cols}"
+
+
+def matvec_weights(t, rows, cols) -> np.ndarray:
+    return fwgpu.synth_matrix(t, rows, cols, seed=1000 + 7 * t + rows + 3 * cols, scale_std=0.02)
+
+
+def matvec_x(t, rows, cols) -> np.ndarray:
+    return fwgpu.randn(2000 + t + cols, cols, 1.0)
+
+
+# dequant fixtures: every code with a spread of fp16 scales incl. zero, subnormal, max
+DEQUANT_SCALES = [0x0000, 0x8000, 0x0001, 0x0003, 0x01FF, 0x03FF, 0x8001, 0x0400, 0x3C00, 0xBC00,
+                  0x2E66, 0x1A3F, 0x7BFF, 0xFBFF, 0x3555, 0x0A00]
+
+
+def dequant_blocks(t) -> np.ndarray:
+    bb = fwgpu.BLOCK_BYTES[t]
+    rng = np.random.default_rng(100 + t)
+    blocks = []
+    for s in DEQUANT_SCALES:
+        for k in range(8):
+            b = np.zeros(bb, np.uint8)
+            b[0], b[1] = s & 0xFF, s >> 8
+            if t == Q8:
+                b[2:] = (np.arange(32) + 32 * k).astype(np.uint8)          # all 256 codes
+            else:
+                b[2:] = rng.integers(0, 256, bb - 2).astype(np.uint8)
+            blocks.append(b)
+    return np.concatenate(blocks)
+
+
+NORM_EPS = 1e-5
+NORM_SIZES = [4, 288, 4096, 8192]
+
+
+def norm_inputs(n):
+    x = fwgpu.randn(300 + n, n, 1.0)
+    w = (fwgpu.randn(400 + n, n, 0.01) + np.float32(1.0)).astype(np.float32)
+    return x, w
+
+
+ROPE_TABLES = [(64, 48, 10000.0), (64, 128, 500000.0), (16, 64, 10000.0)]
+ROPE_CASES = [(0, 6, 48, 64, 10000.0, 0), (17, 6, 48, 64, 10000.0, 0), (63, 8, 128, 64, 500000.0, 0),
+              (5, 2, 64, 16, 10000.0, 1)]
+
+
+def rope_input(nh, hd):
+    return fwgpu.randn(500 + nh * hd, nh * hd, 1.0)
+
+
+def silu_input():
+    x = fwgpu.randn(600, 4096, 3.0)
+    special = np.array([0.0, -0.0, 1e-30, -1e-30, 1e-40, -1e-40, 88.0, -88.0, 89.0, -89.0, 100.0, -100.0,
+                        20.0, -20.0, 1.0, -1.0, 0.5, -0.5, 3.4e38, -3.4e38], np.float32)
+    return np.concatenate([special, x]).astype(np.float32)
+
+
+DOT_SIZES = list(range(1, 68)) + [128, 288, 4096, 14336]
+
+
+def dot_inputs(n):
+    return fwgpu.randn(700 + n, n, 1.0), fwgpu.randn(800 + n, n, 1.0)
+
+
+def argmax_cases():
+    rng = np.random.default_rng(9)
+    cases = [np.array([1, 2, 3, 4, 5], np.float32),
+             np.array([5, 5, 5], np.float32),
+             np.array([1, 7, 3, 7, 7, 2], np.float32),
+             np.array([np.nan, 1, 2], np.float32),
+             np.array([1, np.nan, 2, np.nan], np.float32),
+             np.array([-np.inf, -np.inf], np.float32),
+             np.array([-1.0, -0.0, 0.0, -0.5], np.float32),
+             np.array([0.0, -0.0], np.float32),
+             rng.standard_normal(32000).astype(np.float32),
+             rng.standard_normal(128256).astype(np.float32)]
+    big = rng.standard_normal(128256).astype(np.float32)
+    big[[5, 90000, 128255]] = 9.0
+    cases.append(big)
+    return cases

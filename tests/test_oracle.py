@@ -1,0 +1,296 @@
+"""The oracle (oracle/fw_cpu.c) pinned against forword.c: its own unit-test
+KATs (test_runner.c), golden vectors from the compiled reference
+(tests/golden/, written by make_golden.py) and closed forms / invariants for
+what the reference cannot produce (Q4_0)."""
+import hashlib
+
+import numpy as np
+import pytest
+
+import fw_cpu
+import fwgpu
+import golden_specs as gs
+from conftest import gold_model
+
+Q4, Q5, Q8 = fwgpu.GGML_Q4_0, fwgpu.GGML_Q5_0, fwgpu.GGML_Q8_0
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+# ── reference KATs (test_runner.c) ─────────────────────────────────────────────
+
+def test_kat_rms_norm_unit_mean_square():                      # test_runner.c:30-41
+    out = fw_cpu.rms_norm(np.array([1, 2, 3, 4], np.float32), np.ones(4, np.float32), 1e-5)
+    assert abs(float(np.mean(out.astype(np.float32) ** 2)) - 1.0) < 1e-4
+
+
+def test_kat_rope_pos0_identity():                             # test_runner.c:60-90
+    H = fwgpu.host_lib()
+    cos = np.zeros(16 * 32, np.float32)
+    sin = np.zeros(16 * 32, np.float32)
+    H.fwh_rope_tables(cos.ctypes.data_as(fwgpu.fp), sin.ctypes.data_as(fwgpu.fp), 16, 64, 10000.0)
+    assert np.all(np.abs(cos[:32] - 1) < 1e-6) and np.all(np.abs(sin[:32]) < 1e-6)
+    qk = np.arange(1, 65, dtype=np.float32)
+    assert np.all(np.abs(fw_cpu.rope_apply(qk, 0, 1, 64, cos, sin) - qk) < 1e-5)
+
+
+def test_kat_argmax_and_softmax():                             # test_runner.c:93-107
+    x = np.array([1, 2, 3, 4, 5], np.float32)
+    assert fw_cpu.argmax(x) == 4
+    p = fw_cpu.softmax(x)
+    assert np.all(p > 0) and abs(float(p.sum()) - 1) < 1e-5
+
+
+def test_kat_q8_0_decode():                                    # test_runner.c:110-126
+    blk = np.zeros(34, np.uint8)
+    blk[1] = 0x3C
+    blk[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    assert np.array_equal(fw_cpu.dequant(blk, Q8), np.arange(32, dtype=np.float32) - 16)
+
+
+def test_kat_q8_0_matvec_64():                                 # test_runner.c:161-178
+    blk = np.zeros(34, np.uint8)
+    blk[1] = 0x3C
+    blk[2:] = 2
+    rc, y = fw_cpu.quant_matvec(blk, Q8, np.ones(32, np.float32), 1)
+    assert rc == 0 and abs(y[0] - 64.0) < 1e-4
+
+
+def test_kat_simd_dot_lengths():                               # test_runner.c:207-223
+    a = (np.arange(67) % 7 - 3).astype(np.float32)
+    b = (np.arange(67) % 5 + 1.5).astype(np.float32)
+    for n in range(1, 68):
+        exp = np.float32(0)
+        for i in range(n):
+            exp = np.float32(exp + np.float32(a[i] * b[i]))
+        assert abs(float(fw_cpu.dot(a[:n], b[:n]) - exp)) < 1e-4
+
+
+def test_kat_tensor_matvec_f32():                              # test_runner.c:250-265
+    W = np.array([[1, 2, 3, 4, 5], [2, 0, 1, -1, 3], [-1, 1, -1, 1, 0]], np.float32)
+    x = np.array([1, -2, 3, -4, 5], np.float32)
+    y = np.zeros(3, np.float32)
+    rc = fw_cpu.lib().fwc_tensor_matvec_f32(W.ctypes.data_as(fw_cpu.fp), x.ctypes.data_as(fw_cpu.fp),
+                                            y.ctypes.data_as(fw_cpu.fp), 3, 5)
+    assert rc == 0 and np.allclose(y, [15, 24, -10], atol=1e-4)
+
+
+# ── fp16 and dequantisation ────────────────────────────────────────────────────
+
+def test_half_to_float_all_65536():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = fw_cpu.half_to_float_n(h)
+    lib = h.view(np.float16).astype(np.float32)   # numpy's exact conversion
+    assert np.array_equal(bits(ours), bits(lib))
+
+
+def test_dequant_q8_0_matches_reference(gold_dequant):
+    blocks = gold_dequant[f"blocks_{Q8}"]
+    assert np.array_equal(blocks, gs.dequant_blocks(Q8))
+    out = fw_cpu.dequant(blocks, Q8)
+    assert np.array_equal(bits(out), bits(gold_dequant[f"getrow_{Q8}"]))
+    assert np.array_equal(bits(out), bits(gold_dequant["q8dec"]))
+
+
+def test_dequant_q5_0_matches_reference(gold_dequant):
+    blocks = gold_dequant[f"blocks_{Q5}"]
+    assert np.array_equal(blocks, gs.dequant_blocks(Q5))
+    assert np.array_equal(bits(fw_cpu.dequant(blocks, Q5)), bits(gold_dequant[f"getrow_{Q5}"]))
+
+
+def _closed_form(blocks, t):
+    """Dequantisation written independently from the GGUF block definitions."""
+    bb = fwgpu.BLOCK_BYTES[t]
+    b = blocks.reshape(-1, bb)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)[:, 0]
+    if t == Q8:
+        q = b[:, 2:].view(np.int8).astype(np.float32)
+    else:
+        qs = b[:, 2:] if t == Q4 else b[:, 6:]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int32)
+        if t == Q5:
+            qh = b[:, 2:6].copy().view(np.uint32)[:, 0]
+            hb = (qh[:, None] >> np.arange(32, dtype=np.uint32)[None, :]) & 1
+            q = q | (hb.astype(np.int32) << 4)
+            q = q - 16
+        else:
+            q = q - 8
+        q = q.astype(np.float32)
+    return (d[:, None] * q).astype(np.float32).reshape(-1)
+
+
+@pytest.mark.parametrize("t", [Q4, Q5, Q8])
+def test_dequant_closed_form_all_codes(t):
+    blocks = fwgpu.synth_matrix(t, 64, 256, seed=11 + t, subnormal_every=5)
+    extra = gs.dequant_blocks(t) if t != Q4 else None
+    if t == Q4:   # every code at every nibble position with special scales
+        rows = []
+        for s in gs.DEQUANT_SCALES:
+            for k in range(16):
+                b = np.zeros(18, np.uint8)
+                b[0], b[1] = s & 0xFF, s >> 8
+                lo = (np.arange(16) + k) % 16
+                hi = (np.arange(16) + 2 * k + 1) % 16
+                b[2:] = (lo | (hi << 4)).astype(np.uint8)
+                rows.append(b)
+        extra = np.concatenate(rows)
+    for blk in (blocks, extra):
+        ours = fw_cpu.dequant(blk, t)
+        ref = _closed_form(blk, t)
+        assert np.array_equal(bits(ours), bits(ref))
+
+
+def test_dequant_rejects_bad_sizes():
+    with pytest.raises(ValueError):
+        fw_cpu.dequant(np.zeros(35, np.uint8), Q8)
+
+
+# ── quant_matvec ───────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("case", gs.MATVEC_CASES, ids=lambda c: gs.matvec_key(*c))
+def test_quant_matvec_matches_reference(case, gold_matvec, manifest):
+    t, rows, cols = case
+    w, x = gs.matvec_weights(t, rows, cols), gs.matvec_x(t, rows, cols)
+    key = gs.matvec_key(t, rows, cols)
+    assert hashlib.sha256(w).hexdigest() == manifest["matvec"][key]["w_sha256"]
+    assert hashlib.sha256(x).hexdigest() == manifest["matvec"][key]["x_sha256"]
+    fw_cpu.set_threads(8)
+    rc, y = fw_cpu.quant_matvec(w, t, x, rows)
+    assert rc == 0
+    assert np.array_equal(bits(y), bits(gold_matvec[key]))
+
+
+def test_quant_matvec_q4_0_invariants():
+    """Q4_0 has no reference implementation: pin it by closed form, one-hot
+    columns (exact), linearity under x*2 (exact) and a float64 bound."""
+    rows, cols = 96, 4096
+    w = fwgpu.synth_matrix(Q4, rows, cols, seed=5)
+    W = _closed_form(w, Q4).reshape(rows, cols).astype(np.float64)
+    x = fwgpu.randn(6, cols)
+    rc, y = fw_cpu.quant_matvec(w, Q4, x, rows)
+    assert rc == 0
+    ref = W @ x.astype(np.float64)
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(W) @ np.abs(x.astype(np.float64)))
+    rc, y2 = fw_cpu.quant_matvec(w, Q4, x * np.float32(2), rows)
+    assert np.array_equal(bits(y2), bits(y * np.float32(2)))
+    for j in (0, 31, 32, 1000, cols - 1):
+        e = np.zeros(cols, np.float32)
+        e[j] = 1
+        rc, yj = fw_cpu.quant_matvec(w, Q4, e, rows)
+        assert np.array_equal(bits(yj), bits(W[:, j].astype(np.float32)))
+
+
+def test_quant_matvec_argument_checks():
+    w = np.zeros(34 * 4, np.uint8)
+    x = np.ones(64, np.float32)
+    assert fw_cpu.quant_matvec(w, 3, x, 2)[0] == -1                # unknown type (Q4_1)
+    assert fw_cpu.quant_matvec(w, Q8, x[:40], 2)[0] == -1         # in % 32
+    assert fw_cpu.quant_matvec(w, Q8, x, 3)[0] == -1              # weights too small
+    assert fw_cpu.quant_matvec(w, Q8, x, 2)[0] == 0
+
+
+# ── elementwise / reductions ───────────────────────────────────────────────────
+
+@pytest.mark.parametrize("n", gs.NORM_SIZES)
+def test_rms_norm_matches_reference(n, gold_ops):
+    x, w = gs.norm_inputs(n)
+    assert np.array_equal(bits(fw_cpu.rms_norm(x, w, gs.NORM_EPS)), bits(gold_ops[f"rmsnorm_{n}"]))
+
+
+@pytest.mark.parametrize("tab", gs.ROPE_TABLES)
+def test_host_rope_tables_match_reference(tab, gold_ops):
+    nctx, hd, base = tab
+    cos = np.zeros(nctx * hd // 2, np.float32)
+    sin = np.zeros_like(cos)
+    fwgpu.host_lib().fwh_rope_tables(cos.ctypes.data_as(fwgpu.fp), sin.ctypes.data_as(fwgpu.fp), nctx,
+                                     hd, base)
+    ref = gold_ops[f"ropetab_{nctx}_{hd}_{int(base)}"]
+    assert np.array_equal(bits(np.concatenate([cos, sin])), bits(ref))
+
+
+@pytest.mark.parametrize("case", gs.ROPE_CASES)
+def test_rope_apply_matches_reference(case, gold_ops):
+    pos, nh, hd, nctx, base, neox = case
+    cos = np.zeros(nctx * hd // 2, np.float32)
+    sin = np.zeros_like(cos)
+    fwgpu.host_lib().fwh_rope_tables(cos.ctypes.data_as(fwgpu.fp), sin.ctypes.data_as(fwgpu.fp), nctx,
+                                     hd, base)
+    out = fw_cpu.rope_apply(gs.rope_input(nh, hd), pos, nh, hd, cos, sin, neox)
+    assert np.array_equal(bits(out), bits(gold_ops[f"rope_{pos}_{nh}_{hd}_{int(base)}_{neox}"]))
+
+
+def test_silu_matches_reference(gold_ops):
+    assert np.array_equal(bits(fw_cpu.silu(gs.silu_input())), bits(gold_ops["silu"]))
+
+
+def test_dot_matches_reference(gold_ops):
+    got = np.array([fw_cpu.dot(*gs.dot_inputs(n)) for n in gs.DOT_SIZES], np.float32)
+    assert np.array_equal(bits(got), bits(gold_ops["dot"]))
+
+
+def test_argmax_matches_reference(gold_ops):
+    got = [fw_cpu.argmax(c) for c in gs.argmax_cases()]
+    assert got == gold_ops["argmax"].tolist()
+    assert got[:8] == [4, 0, 1, 0, 2, 0, 1, 0]   # strict '>' scan: ties -> lowest, NaN never wins
+
+
+def test_attention_core_float64_bound():
+    """Softmax attention with GQA head mapping h -> h / (n_head/n_kv), against float64 numpy."""
+    n_head, n_kv, hd, pos = 8, 2, 64, 37
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    kc = rng.standard_normal((pos + 1) * n_kv * hd).astype(np.float32)
+    vc = rng.standard_normal((pos + 1) * n_kv * hd).astype(np.float32)
+    out = fw_cpu.attention_core(q, kc, vc, n_head, n_kv, hd, pos)
+    K = kc.reshape(pos + 1, n_kv, hd).astype(np.float64)
+    V = vc.reshape(pos + 1, n_kv, hd).astype(np.float64)
+    Q = q.reshape(n_head, hd).astype(np.float64)
+    ref = np.zeros((n_head, hd))
+    for h in range(n_head):
+        g = h // (n_head // n_kv)
+        s = K[:, g, :] @ Q[h] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        ref[h] = (p / p.sum()) @ V[:, g, :]
+    assert np.max(np.abs(out - ref.reshape(-1))) < 1e-5
+
+
+# ── whole forward vs the reference's transformer_forward ──────────────────────
+
+@pytest.mark.parametrize("name", list(gs.MODELS))
+def test_forward_matches_reference(name, manifest):
+    m = gs.MODELS[name]
+    gold = gold_model(name)
+    sp = m["spec"]()
+    host = fwgpu.HostModel(synth=sp, max_ctx=m["max_ctx"])
+    try:
+        img = np.ctypeslib.as_array((fwgpu.C.c_uint8 * host._synth[1]).from_address(host._synth[0]))
+        assert hashlib.sha256(img).hexdigest() == manifest["models"][name]["gguf_sha256"]
+        prompt = gs.prompt(name)
+        assert prompt.tolist() == manifest["models"][name]["prompt"]
+        fw_cpu.set_threads(4)
+        with fw_cpu.OracleModel(host) as om:
+            toks = list(prompt)
+            lsteps, tsteps = gs.logit_steps(name), gs.trace_steps(name)
+            for f in range(gs.n_forwards(name)):
+                lg = om.forward(int(toks[f]), f)
+                if f in lsteps:
+                    assert np.array_equal(bits(lg), bits(gold[f"logits_{f}"])), f"logits at forward {f}"
+                if f in tsteps:
+                    assert np.array_equal(bits(om.trace().reshape(-1)), bits(gold[f"trace_{f}"]))
+                nxt = fw_cpu.argmax(lg)
+                assert nxt == int(gold["stats"][f, 0])
+                if f + 1 >= len(prompt):
+                    toks.append(nxt)
+            assert np.array_equal(np.array(toks, np.uint32), gold["tokens"])
+    finally:
+        host.close()
+
+
+def test_forward_rejects_out_of_range():                       # transformer.c:156-164
+    m = gs.MODELS["gqa"]
+    with fwgpu.HostModel(synth=m["spec"]()) as host, fw_cpu.OracleModel(host) as om:
+        assert not om.forward_raw(0, host.n_ctx)
+        assert not om.forward_raw(host.cfg.n_vocab, 0)
+        assert om.forward_raw(host.cfg.n_vocab - 1, host.n_ctx - 1)
