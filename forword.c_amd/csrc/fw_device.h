@@ -1,0 +1,219 @@
+// Device-side building blocks shared by the gfx950 kernels of the decode path.
+//
+// GGUF blocks are read in place from the uploaded data section:
+//   Q4_0 18 B = fp16 d | qs[16]          w_j = d*(q_j - 8), q_j = qs[j]&15, q_{j+16} = qs[j]>>4
+//   Q5_0 22 B = fp16 d | qh u32 | qs[16]  5th bit of code j = bit j of qh, w_j = d*(q_j - 16)
+//   Q8_0 34 B = fp16 d | int8 qs[32]      w_j = d*q_j
+// (gguf.c:211-215; quant_matvec.c:192-229; quant.c:232-263).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fw_kernels.h"
+
+namespace fw {
+
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// Vector types that only promise dword alignment: GGUF blocks are 18/22/34 B,
+// so a pair of blocks starts on a 4-byte boundary but rarely on 16.
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+typedef u32x2 u32x2_a4 __attribute__((aligned(4)));
+
+template <uint32_t T> struct Blk;
+template <> struct Blk<kQ4_0> { static constexpr int bytes = 18, pair_dw = 9; };
+template <> struct Blk<kQ5_0> { static constexpr int bytes = 22, pair_dw = 11; };
+template <> struct Blk<kQ8_0> { static constexpr int bytes = 34, pair_dw = 17; };
+
+// fp16 bits (low half of h) -> fp32, exact incl. subnormals (v_cvt_f32_f16 with
+// fp16 denormals enabled, the gfx9 default).
+__device__ __forceinline__ float h2f(uint32_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu));
+}
+
+__device__ __forceinline__ uint32_t align16(uint32_t hi, uint32_t lo)
+{
+    return __builtin_amdgcn_alignbit(hi, lo, 16);
+}
+
+// Two codes q in 0..15, one per byte in the selected 16-bit half of v, to
+// floats q/512: a byte holding 0..15 read as OCP e4m3 is exactly q * 2^-9.
+template <bool HI_HALF>
+__device__ __forceinline__ float2v nib2(uint32_t v)
+{
+    return __builtin_amdgcn_cvt_pk_f32_fp8((int)v, HI_HALF);
+}
+
+// d * sum_j (q_j - 8) x_j over one Q4_0 block; q[4] = the 16 code bytes, x[32].
+__device__ __forceinline__ float dot_q4_0(float d, const uint32_t *q, const float *x, float sx)
+{
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        uint32_t lo = q[w] & 0x0F0F0F0Fu, hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+        float2v l01 = nib2<false>(lo), l23 = nib2<true>(lo);
+        float2v h01 = nib2<false>(hi), h23 = nib2<true>(hi);
+        a0 = __builtin_fmaf(l01.x, x[4 * w + 0], a0);
+        a1 = __builtin_fmaf(l01.y, x[4 * w + 1], a1);
+        a2 = __builtin_fmaf(l23.x, x[4 * w + 2], a2);
+        a3 = __builtin_fmaf(l23.y, x[4 * w + 3], a3);
+        a0 = __builtin_fmaf(h01.x, x[16 + 4 * w + 0], a0);
+        a1 = __builtin_fmaf(h01.y, x[16 + 4 * w + 1], a1);
+        a2 = __builtin_fmaf(h23.x, x[16 + 4 * w + 2], a2);
+        a3 = __builtin_fmaf(h23.y, x[16 + 4 * w + 3], a3);
+    }
+    float s = (a0 + a1) + (a2 + a3);              // sum q_j x_j / 512
+    return d * __builtin_fmaf(s, 512.0f, -8.0f * sx);
+}
+
+// d * sum_j (q_j - 16) x_j over one Q5_0 block.
+__device__ __forceinline__ float dot_q5_0(float d, uint32_t qh, const uint32_t *q, const float *x,
+                                          float sx)
+{
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        uint32_t lo = q[w] & 0x0F0F0F0Fu, hi = (q[w] >> 4) & 0x0F0F0F0Fu;
+        float2v l01 = nib2<false>(lo), l23 = nib2<true>(lo);
+        float2v h01 = nib2<false>(hi), h23 = nib2<true>(hi);
+        a0 = __builtin_fmaf(l01.x, x[4 * w + 0], a0);
+        a1 = __builtin_fmaf(l01.y, x[4 * w + 1], a1);
+        a0 = __builtin_fmaf(l23.x, x[4 * w + 2], a0);
+        a1 = __builtin_fmaf(l23.y, x[4 * w + 3], a1);
+        a0 = __builtin_fmaf(h01.x, x[16 + 4 * w + 0], a0);
+        a1 = __builtin_fmaf(h01.y, x[16 + 4 * w + 1], a1);
+        a0 = __builtin_fmaf(h23.x, x[16 + 4 * w + 2], a0);
+        a1 = __builtin_fmaf(h23.y, x[16 + 4 * w + 3], a1);
+    }
+#pragma unroll
+    for (int j = 0; j < 32; j += 2) {
+        b0 = __builtin_fmaf((float)((qh >> j) & 1u), x[j], b0);
+        b1 = __builtin_fmaf((float)((qh >> (j + 1)) & 1u), x[j + 1], b1);
+    }
+    float s = a0 + a1, hb = b0 + b1;               // sum lo_j x_j / 512, sum hb_j x_j
+    return d * (__builtin_fmaf(s, 512.0f, __builtin_fmaf(hb, 16.0f, -16.0f * sx)));
+}
+
+// d * sum_j q_j x_j over one Q8_0 block; q[8] = the 32 code bytes.
+__device__ __forceinline__ float dot_q8_0(float d, const uint32_t *q, const float *x)
+{
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t v = q[k];
+        a0 = __builtin_fmaf((float)((int32_t)(v << 24) >> 24), x[4 * k + 0], a0);
+        a1 = __builtin_fmaf((float)((int32_t)(v << 16) >> 24), x[4 * k + 1], a1);
+        a2 = __builtin_fmaf((float)((int32_t)(v << 8) >> 24), x[4 * k + 2], a2);
+        a3 = __builtin_fmaf((float)((int32_t)v >> 24), x[4 * k + 3], a3);
+    }
+    return d * ((a0 + a1) + (a2 + a3));
+}
+
+// Dot of a 4-byte-aligned pair of blocks (2*32 columns) with x[64].
+template <uint32_t T>
+__device__ __forceinline__ float dot_pair(const uint32_t *dw, const float *x, float sx0, float sx1)
+{
+    if constexpr (T == kQ4_0) {
+        uint32_t q0[4] = { align16(dw[1], dw[0]), align16(dw[2], dw[1]), align16(dw[3], dw[2]),
+                           align16(dw[4], dw[3]) };
+        uint32_t q1[4] = { dw[5], dw[6], dw[7], dw[8] };
+        return dot_q4_0(h2f(dw[0]), q0, x, sx0) + dot_q4_0(h2f(dw[4] >> 16), q1, x + 32, sx1);
+    } else if constexpr (T == kQ5_0) {
+        uint32_t qh0 = align16(dw[1], dw[0]);
+        uint32_t q0[4] = { align16(dw[2], dw[1]), align16(dw[3], dw[2]), align16(dw[4], dw[3]),
+                           align16(dw[5], dw[4]) };
+        uint32_t q1[4] = { dw[7], dw[8], dw[9], dw[10] };
+        return dot_q5_0(h2f(dw[0]), qh0, q0, x, sx0) + dot_q5_0(h2f(dw[5] >> 16), dw[6], q1, x + 32, sx1);
+    } else {
+        uint32_t q0[8], q1[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) { q0[k] = align16(dw[k + 1], dw[k]); q1[k] = dw[9 + k]; }
+        return dot_q8_0(h2f(dw[0]), q0, x) + dot_q8_0(h2f(dw[8] >> 16), q1, x + 32);
+    }
+}
+
+// Load one pair of blocks (pair_dw dwords) from a dword-aligned address.
+template <uint32_t T>
+__device__ __forceinline__ void load_pair(const uint8_t *p, uint32_t *dw)
+{
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(p);
+    if constexpr (T == kQ4_0) {                       // 36 B = 16 + 16 + 4
+        u32x4 a = *reinterpret_cast<const u32x4_a4 *>(w);
+        u32x4 b = *reinterpret_cast<const u32x4_a4 *>(w + 4);
+        dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+        dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
+        dw[8] = w[8];
+    } else if constexpr (T == kQ5_0) {                // 44 B = 16 + 16 + 8 + 4
+        u32x4 a = *reinterpret_cast<const u32x4_a4 *>(w);
+        u32x4 b = *reinterpret_cast<const u32x4_a4 *>(w + 4);
+        u32x2 c = *reinterpret_cast<const u32x2_a4 *>(w + 8);
+        dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+        dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
+        dw[8] = c.x; dw[9] = c.y; dw[10] = w[10];
+    } else {                                          // 68 B = 4*16 + 4
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            u32x4 a = *reinterpret_cast<const u32x4_a4 *>(w + 4 * k);
+            dw[4 * k] = a.x; dw[4 * k + 1] = a.y; dw[4 * k + 2] = a.z; dw[4 * k + 3] = a.w;
+        }
+        dw[16] = w[16];
+    }
+}
+
+// One block from a 2-byte-aligned address (rows whose byte length is not a
+// multiple of 4, e.g. 9 blocks of 34 B): 16-bit loads, reassembled.
+template <uint32_t T>
+__device__ __forceinline__ float dot_single(const uint8_t *p, const float *x, float sx)
+{
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+    if constexpr (T == kQ4_0) {
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = (uint32_t)h[1 + 2 * k] | ((uint32_t)h[2 + 2 * k] << 16);
+        return dot_q4_0(h2f(h[0]), q, x, sx);
+    } else if constexpr (T == kQ5_0) {
+        uint32_t q[4];
+        uint32_t qh = (uint32_t)h[1] | ((uint32_t)h[2] << 16);
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = (uint32_t)h[3 + 2 * k] | ((uint32_t)h[4 + 2 * k] << 16);
+        return dot_q5_0(h2f(h[0]), qh, q, x, sx);
+    } else {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) q[k] = (uint32_t)h[1 + 2 * k] | ((uint32_t)h[2 + 2 * k] << 16);
+        return dot_q8_0(h2f(h[0]), q, x);
+    }
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// expf through double precision: the float result is the correctly rounded
+// e^v except where the double lands within an ulp of a float rounding midpoint.
+__device__ __forceinline__ float exp_f32(float v) { return (float)exp((double)v); }
+
+// apply_silu (ffn.c:17-25): v * sigma(v) with the reference's two branches.
+__device__ __forceinline__ float silu_ref(float v)
+{
+    float sig;
+    if (v >= 0.0f) sig = 1.0f / (1.0f + exp_f32(-v));
+    else { float e = exp_f32(v); sig = e / (1.0f + e); }
+    return v * sig;
+}
+
+} // namespace fw

@@ -1,0 +1,85 @@
+// Host-side launch interface of the gfx950 kernels (internal to libforword_gpu.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fw {
+
+// ggml type ids on the path (gguf.c:155-174)
+enum : uint32_t { kF32 = 0, kQ4_0 = 2, kQ5_0 = 6, kQ8_0 = 8 };
+
+// Device-resident step state read by every kernel of a token step, so one
+// captured graph serves every position.
+struct StepState {
+    uint32_t token;      // token fed at this step
+    uint32_t pos;        // its position
+    uint32_t n_prompt;   // greedy loop: prompt length
+    uint32_t next;       // argmax of this step's logits
+    uint32_t greedy;     // 1 inside generate_greedy: advance token/pos on device
+    uint32_t pad[3];
+};
+
+enum Epi : int { EPI_STORE = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
+
+// One GEMV launch over up to three weight matrices that share the input x and
+// the column count (fused QKV; gate+up).  Rows of matrix s are rows[s].
+struct QmvArgs {
+    const uint8_t *w[3];
+    uint32_t rows[3];
+    uint32_t n_seg;
+    uint32_t role_base;        // QKV: role of matrix 0 (0 = Q, 1 = K, 2 = V) when launched apart
+    uint32_t n_cols;
+    uint64_t row_bytes;
+    uint32_t n_groups;
+    uint32_t group_base[4];
+    const float *x;
+    float *out[3];             // STORE: per-matrix outputs; QKV: by role q, K cache, V cache (layer slices)
+                               // RESID: residual stream x (updated in place); SWIGLU: h
+    float *trace;              // RESID: copy of the updated residual (may be null)
+    const float *cos_tab, *sin_tab;
+    const StepState *state;
+    uint32_t head_dim;
+    uint32_t kv_dim;           // n_head_kv * head_dim (K/V cache row length)
+};
+
+// Rows computed by one wave of the GEMV kernels.
+constexpr int kRowsPerWave = 4;
+
+hipError_t launch_qmv(uint32_t type, int epi, QmvArgs a, hipStream_t s);
+// Fill group bookkeeping of QmvArgs for the given epilogue.
+void qmv_plan(QmvArgs &a, int epi);
+// Whether matrices of this type/column count/base alignment use the
+// paired-block (dword-aligned) path.
+bool qmv_pair_ok(uint32_t type, uint32_t n_cols, const void *base);
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n, float eps,
+                          hipStream_t s);
+hipError_t launch_embed(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
+                        const StepState *st, const uint32_t *token_override, float embd_scale, float *x,
+                        hipStream_t s);
+hipError_t launch_get_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t row, float *out,
+                          hipStream_t s);
+hipError_t launch_dequant(const uint8_t *blocks, uint32_t type, uint64_t n_blocks, float *out,
+                          hipStream_t s);
+
+// Split-K decode attention: partials [n_head][n_splits][head_dim + 2], then combine.
+uint32_t attn_splits(uint32_t max_ctx, uint32_t n_kv);
+bool attn_supported(uint32_t head_dim, uint32_t group);
+hipError_t launch_attention(const float *q, const float *kc, const float *vc, float *part, float *out,
+                            uint32_t n_head, uint32_t n_kv, uint32_t head_dim, uint32_t n_splits,
+                            const StepState *st, uint32_t pos_host, hipStream_t s);
+
+hipError_t launch_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *counter,
+                         uint32_t *out, StepState *st, const uint32_t *prompt, uint32_t *ids,
+                         uint32_t n_blocks, hipStream_t s);
+uint32_t argmax_blocks(uint32_t n);
+
+hipError_t launch_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t head_dim, const float *cos_tab,
+                       const float *sin_tab, int neox, hipStream_t s);
+hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s);
+hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s);
+hipError_t launch_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);
+
+} // namespace fw

@@ -1,0 +1,683 @@
+// gfx950 kernels of the forword decode path.
+//
+// GEMV (quant_matvec.c:263-312 and the fused callers attention.c:124-166,
+// ffn.c:82-106, transformer.c:271-288): one wave computes kRowsPerWave output
+// rows; each lane walks the row in pairs of blocks (64 columns, a 4-byte
+// aligned 36/44/68-byte chunk) with dword-aligned 128-bit loads, keeps the
+// matching 64 activations in registers for all rows of the wave, and the
+// partial sums meet in a cross-lane reduction.  Block scales are applied once
+// per block; Q4_0/Q5_0 codes are unpacked two per instruction.  Epilogues fuse
+// RoPE + KV append (QKV), the residual add (Wo, down) and SiLU(gate)*up.
+//
+// Attention (attention.c:142-164): split-K over positions ("flash decoding"),
+// one workgroup per (KV head, split) serving all query heads of its GQA group
+// from a single read of K/V, online softmax in the log2 domain, then a combine
+// kernel per query head.
+#include "fw_device.h"
+#include "fw_kernels.h"
+
+#include <math.h>
+
+namespace fw {
+
+// ── GEMV ─────────────────────────────────────────────────────────────────────
+
+template <uint32_t T, int EPI, bool PAIR>
+__global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
+{
+    constexpr int R = kRowsPerWave;
+    const int lane = threadIdx.x & 63;
+    const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= a.n_groups) return;
+    if (EPI == EPI_STORE && a.state && a.state->greedy && a.state->pos + 1 < a.state->n_prompt)
+        return;   // greedy prefill: these logits are never read
+
+    int seg = 0;
+    if (EPI != EPI_SWIGLU)
+        while (seg + 1 < (int)a.n_seg && g >= a.group_base[seg + 1]) seg++;
+    const uint8_t *wr[R];
+    bool ok[R];
+    uint32_t row[R];
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+        int s = seg;
+        if (EPI == EPI_SWIGLU) { s = k < R / 2 ? 0 : 1; row[k] = g * (R / 2) + (k % (R / 2)); }
+        else row[k] = (g - a.group_base[seg]) * R + k;
+        ok[k] = row[k] < a.rows[s];
+        wr[k] = a.w[s] + (size_t)(ok[k] ? row[k] : 0) * a.row_bytes;
+    }
+
+    float acc[R];
+#pragma unroll
+    for (int k = 0; k < R; k++) acc[k] = 0.0f;
+    const bool xv4 = ((uintptr_t)a.x & 15) == 0;
+
+    if constexpr (T == kF32) {
+        for (uint32_t c = lane; c < a.n_cols; c += 64) {
+            float xc = a.x[c];
+#pragma unroll
+            for (int k = 0; k < R; k++)
+                if (ok[k]) acc[k] = __builtin_fmaf(reinterpret_cast<const float *>(wr[k])[c], xc, acc[k]);
+        }
+    } else if constexpr (PAIR) {
+        constexpr int BB = Blk<T>::bytes, NDW = Blk<T>::pair_dw;
+        const uint32_t n_pairs = a.n_cols / 64;
+        for (uint32_t p = lane; p < n_pairs; p += 64) {
+            float xv[64];
+            const float *xp = a.x + 64 * (size_t)p;
+            if (xv4) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    float4 v = reinterpret_cast<const float4 *>(xp)[i];
+                    xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 64; i++) xv[i] = xp[i];
+            }
+            float sx0 = 0.f, sx1 = 0.f;
+            if constexpr (T != kQ8_0) {
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
+                sx0 = s0 + s1;
+                sx1 = s2 + s3;
+            }
+            uint32_t dw[R][NDW];
+#pragma unroll
+            for (int k = 0; k < R; k++)
+                if (ok[k]) load_pair<T>(wr[k] + (size_t)p * (2 * BB), dw[k]);
+#pragma unroll
+            for (int k = 0; k < R; k++)
+                if (ok[k]) acc[k] += dot_pair<T>(dw[k], xv, sx0, sx1);
+        }
+    } else {
+        constexpr int BB = Blk<T>::bytes;
+        const uint32_t n_blocks = a.n_cols / 32;
+        for (uint32_t b = lane; b < n_blocks; b += 64) {
+            float xv[32];
+            const float *xp = a.x + 32 * (size_t)b;
+            if (xv4) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    float4 v = reinterpret_cast<const float4 *>(xp)[i];
+                    xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; i++) xv[i] = xp[i];
+            }
+            float sx = 0.f;
+            if constexpr (T != kQ8_0) {
+                float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; }
+                sx = s0 + s1;
+            }
+#pragma unroll
+            for (int k = 0; k < R; k++)
+                if (ok[k]) acc[k] += dot_single<T>(wr[k] + (size_t)b * BB, xv, sx);
+        }
+    }
+
+#pragma unroll
+    for (int k = 0; k < R; k++) acc[k] = wave_sum(acc[k]);
+    if (lane != 0) return;
+
+    if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+        for (int k = 0; k < R; k++)
+            if (ok[k]) a.out[seg][row[k]] = acc[k];
+    } else if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+        for (int k = 0; k < R; k++)
+            if (ok[k]) {
+                float v = a.out[0][row[k]] + acc[k];          // x[i] += y[i] (transformer.c:271-272)
+                a.out[0][row[k]] = v;
+                if (a.trace) a.trace[row[k]] = v;
+            }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int k = 0; k < R / 2; k++)
+            if (ok[k]) a.out[0][row[k]] = silu_ref(acc[k]) * acc[k + R / 2];   // ffn.c:88-104
+    } else {   // EPI_QKV: RoPE on q and k rows (rope.c:37-43), then q out / KV append at pos
+        const uint32_t pos = a.state->pos, half = a.head_dim / 2;
+        const uint32_t role = seg + a.role_base;
+        float v[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) v[k] = acc[k];
+        if (role < 2) {
+#pragma unroll
+            for (int k = 0; k < R; k += 2) {
+                uint32_t i = (row[k] % a.head_dim) / 2;
+                float c = a.cos_tab[(size_t)pos * half + i], s = a.sin_tab[(size_t)pos * half + i];
+                float v0 = v[k], v1 = v[k + 1];
+                v[k] = v0 * c - v1 * s;
+                v[k + 1] = v0 * s + v1 * c;
+            }
+        }
+        float *dst = role == 0 ? a.out[0] : a.out[role] + (size_t)pos * a.kv_dim;
+#pragma unroll
+        for (int k = 0; k < R; k++)
+            if (ok[k]) dst[row[k]] = v[k];
+    }
+}
+
+void qmv_plan(QmvArgs &a, int epi)
+{
+    const uint32_t R = kRowsPerWave;
+    if (epi == EPI_SWIGLU) {
+        a.n_groups = (a.rows[0] + R / 2 - 1) / (R / 2);
+        a.group_base[0] = 0;
+        a.group_base[1] = a.n_groups;
+        return;
+    }
+    uint32_t base = 0;
+    for (uint32_t s = 0; s < a.n_seg; s++) {
+        a.group_base[s] = base;
+        base += (a.rows[s] + R - 1) / R;
+    }
+    a.group_base[a.n_seg] = base;
+    a.n_groups = base;
+}
+
+bool qmv_pair_ok(uint32_t type, uint32_t n_cols, const void *base)
+{
+    return type != kF32 && n_cols % 64 == 0 && ((uintptr_t)base & 3) == 0;
+}
+
+template <uint32_t T, int EPI>
+static hipError_t launch_t(const QmvArgs &a, bool pair, hipStream_t s)
+{
+    dim3 grid((a.n_groups + 3) / 4), block(256);
+    if (pair) hipLaunchKernelGGL((k_qmv<T, EPI, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_qmv<T, EPI, false>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_e(uint32_t type, const QmvArgs &a, hipStream_t s)
+{
+    bool pair = true;
+    for (uint32_t i = 0; i < (EPI == EPI_SWIGLU ? 2u : a.n_seg); i++)
+        pair = pair && qmv_pair_ok(type, a.n_cols, a.w[i]);
+    switch (type) {
+    case kQ4_0: return launch_t<kQ4_0, EPI>(a, pair, s);
+    case kQ5_0: return launch_t<kQ5_0, EPI>(a, pair, s);
+    case kQ8_0: return launch_t<kQ8_0, EPI>(a, pair, s);
+    case kF32: return launch_t<kF32, EPI>(a, false, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_qmv(uint32_t type, int epi, QmvArgs a, hipStream_t s)
+{
+    if (!a.n_groups) return hipSuccess;
+    switch (epi) {
+    case EPI_STORE: return launch_e<EPI_STORE>(type, a, s);
+    case EPI_QKV: return launch_e<EPI_QKV>(type, a, s);
+    case EPI_RESID: return launch_e<EPI_RESID>(type, a, s);
+    case EPI_SWIGLU: return launch_e<EPI_SWIGLU>(type, a, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ── RMSNorm (norm.c:7-16) with the reference's exact summation order ─────────
+// ss = simd_sum_squares: 16 lane chains of FMAs over stride-16 elements, the
+// two 8-lane halves added, one 8-wide FMA step, the 8->4->2->1 tree
+// (simd.h:27-67), `0.0f + tree` and the scalar tail (simd.h:151-153); then
+// scale = 1.0f/sqrtf(ss/n + eps) and out = (x*w)*scale, each product rounded.
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w,
+                                                  float *__restrict__ out, uint32_t n, float eps)
+{
+    __shared__ float s_scale;
+    if (threadIdx.x < 64) {
+        const int L = threadIdx.x;
+        const uint32_t n16 = n / 16 * 16;
+        float acc = 0.0f;
+        if (L < 16)
+            for (uint32_t i = L; i < n16; i += 16) acc = __builtin_fmaf(x[i], x[i], acc);
+        float hi = __shfl_down(acc, 8, 64);
+        if (L < 8) {
+            acc = acc + hi;
+            if (n16 + 8 <= n) acc = __builtin_fmaf(x[n16 + L], x[n16 + L], acc);
+        }
+        float a4 = __shfl_down(acc, 4, 64);
+        float s = acc + a4;                       // lanes 0..3: lo128 + hi128
+        float s2 = __shfl_down(s, 2, 64);
+        float t = s + s2;                         // lanes 0,1: movehl step
+        float t1 = __shfl_down(t, 1, 64);
+        if (L == 0) {
+            float sum = 0.0f + (t + t1);
+            for (uint32_t i = n / 8 * 8; i < n; i++) sum = sum + x[i] * x[i];
+            s_scale = 1.0f / sqrtf((sum / (float)n) + eps);
+        }
+    }
+    __syncthreads();
+    const float sc = s_scale;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = w ? x[i] * w[i] : x[i];
+        out[i] = v * sc;
+    }
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n, float eps, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, x, w, out, n, eps);
+    return hipGetLastError();
+}
+
+// ── dequantisation: embedding row, get_row, bulk ─────────────────────────────
+
+__device__ __forceinline__ float dequant_one(const uint8_t *blk, uint32_t type, uint32_t j)
+{
+    float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    if (type == kQ8_0) return d * (float)(int8_t)blk[2 + j];                    // quant.c:258
+    if (type == kQ4_0) {
+        uint32_t b = blk[2 + (j & 15)];
+        int q = (int)(j < 16 ? (b & 15u) : (b >> 4));
+        return d * (float)(q - 8);
+    }
+    uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                  ((uint32_t)blk[5] << 24);
+    uint32_t b = blk[6 + (j & 15)];
+    int q = (int)((j < 16 ? (b & 15u) : (b >> 4)) | (((qh >> j) & 1u) << 4));
+    return d * (float)(q - 16);                                                 // quant_matvec.c:204-212
+}
+
+__device__ __forceinline__ uint32_t block_bytes_dev(uint32_t t)
+{
+    return t == kQ4_0 ? 18u : t == kQ5_0 ? 22u : 34u;
+}
+
+__global__ void k_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
+                      const StepState *st, const uint32_t *tok_override, uint32_t row_fixed,
+                      float embd_scale, float *out)
+{
+    uint32_t row = st ? st->token : (tok_override ? *tok_override : row_fixed);
+    if (row >= n_rows) row = n_rows - 1;            // bounds were checked on the host
+    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n_cols; j += gridDim.x * blockDim.x) {
+        float v;
+        if (type == kF32) v = reinterpret_cast<const float *>(w)[(size_t)row * n_cols + j];
+        else {
+            uint32_t bb = block_bytes_dev(type);
+            const uint8_t *blk = w + (size_t)row * (n_cols / 32) * bb + (size_t)(j / 32) * bb;
+            v = dequant_one(blk, type, j & 31);
+        }
+        if (embd_scale != 1.0f) v *= embd_scale;
+        out[j] = v;
+    }
+}
+
+hipError_t launch_embed(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
+                        const StepState *st, const uint32_t *token_override, float embd_scale, float *x,
+                        hipStream_t s)
+{
+    uint32_t blocks = (n_cols + 255) / 256;
+    hipLaunchKernelGGL(k_row, dim3(blocks), dim3(256), 0, s, w, type, n_cols, n_rows, st, token_override,
+                       0u, embd_scale, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_get_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t row, float *out,
+                          hipStream_t s)
+{
+    uint32_t blocks = (n_cols + 255) / 256;
+    hipLaunchKernelGGL(k_row, dim3(blocks), dim3(256), 0, s, w, type, n_cols, row + 1u,
+                       (const StepState *)nullptr, (const uint32_t *)nullptr, row, 1.0f, out);
+    return hipGetLastError();
+}
+
+__global__ void k_dequant(const uint8_t *blocks, uint32_t type, uint64_t n, float *out)
+{
+    uint32_t bb = block_bytes_dev(type);
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = dequant_one(blocks + (i / 32) * bb, type, (uint32_t)(i & 31));
+}
+
+hipError_t launch_dequant(const uint8_t *blocks, uint32_t type, uint64_t n_blocks, float *out, hipStream_t s)
+{
+    uint64_t n = n_blocks * 32;
+    uint64_t g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    hipLaunchKernelGGL(k_dequant, dim3((uint32_t)g), dim3(256), 0, s, blocks, type, n, out);
+    return hipGetLastError();
+}
+
+// ── attention ────────────────────────────────────────────────────────────────
+
+template <int EPL, int G>
+__global__ __launch_bounds__(256) void k_attn(const float *__restrict__ q, const float *__restrict__ kc,
+                                               const float *__restrict__ vc, float *__restrict__ part,
+                                               uint32_t n_kv, uint32_t n_splits, const StepState *st,
+                                               uint32_t pos_host, float scale_log2)
+{
+    constexpr int HD = 16 * EPL;
+    __shared__ float s_m[4][G], s_l[4][G], s_o[4][G][HD];
+    const uint32_t pos = st ? st->pos : pos_host;
+    const uint32_t kvh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
+    const uint32_t n_pos = pos + 1, chunk = (n_pos + n_splits - 1) / n_splits;
+    const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, l16 = lane & 15;
+    const size_t kvd = (size_t)n_kv * HD;
+
+    float qv[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qv[g][e] = q[(kvh * G + g) * HD + l16 * EPL + e];
+    float m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[g][e] = 0.f;
+    }
+
+    for (uint32_t t = t0 + wave * 4 + grp; t < t1; t += 16) {
+        const float *kp = kc + (size_t)t * kvd + kvh * HD + l16 * EPL;
+        const float *vp = vc + (size_t)t * kvd + kvh * HD + l16 * EPL;
+        float kk[EPL], vv[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) { kk[e] = kp[e]; vv[e] = vp[e]; }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[e], d);
+            d += __shfl_xor(d, 8, 64);
+            d += __shfl_xor(d, 4, 64);
+            d += __shfl_xor(d, 2, 64);
+            d += __shfl_xor(d, 1, 64);
+            float s = d * scale_log2;
+            float mn = fmaxf(m[g], s);
+            float c = exp2f(m[g] - mn), p = exp2f(s - mn);
+            l[g] = __builtin_fmaf(l[g], c, p);
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(o[g][e], c, p * vv[e]);
+            m[g] = mn;
+        }
+    }
+
+    // merge the four 16-lane groups of the wave
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float mw = fmaxf(m[g], __shfl_xor(m[g], 16, 64));
+        mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
+        float c = mw == -INFINITY ? 0.f : exp2f(m[g] - mw);
+        float lw = l[g] * c;
+        lw += __shfl_xor(lw, 16, 64);
+        lw += __shfl_xor(lw, 32, 64);
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            float ov = o[g][e] * c;
+            ov += __shfl_xor(ov, 16, 64);
+            ov += __shfl_xor(ov, 32, 64);
+            o[g][e] = ov;
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) s_o[wave][g][l16 * EPL + e] = o[g][e];
+            if (lane == 0) { s_m[wave][g] = mw; s_l[wave][g] = lw; }
+        }
+    }
+    __syncthreads();
+    // merge the four waves and write this split's partial
+    for (int i = threadIdx.x; i < G * HD; i += 256) {
+        const int g = i / HD, dd = i % HD;
+        float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            float c = M == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+            L = __builtin_fmaf(s_l[w][g], c, L);
+            O = __builtin_fmaf(s_o[w][g][dd], c, O);
+        }
+        float *pp = part + ((size_t)(kvh * G + g) * n_splits + split) * (HD + 2);
+        pp[dd] = O;
+        if (dd == 0) { pp[HD] = M; pp[HD + 1] = L; }
+    }
+}
+
+__global__ void k_attn_combine(const float *__restrict__ part, float *__restrict__ out, uint32_t n_splits,
+                               uint32_t hd)
+{
+    const uint32_t h = blockIdx.x;
+    const float *base = part + (size_t)h * n_splits * (hd + 2);
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < n_splits; s++) M = fmaxf(M, base[(size_t)s * (hd + 2) + hd]);
+    float L = 0.f;
+    for (uint32_t s = 0; s < n_splits; s++) {
+        float ms = base[(size_t)s * (hd + 2) + hd];
+        if (ms != -INFINITY) L = __builtin_fmaf(base[(size_t)s * (hd + 2) + hd + 1], exp2f(ms - M), L);
+    }
+    const float inv = 1.0f / L;
+    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+        float O = 0.f;
+        for (uint32_t s = 0; s < n_splits; s++) {
+            float ms = base[(size_t)s * (hd + 2) + hd];
+            if (ms != -INFINITY) O = __builtin_fmaf(base[(size_t)s * (hd + 2) + d], exp2f(ms - M), O);
+        }
+        out[(size_t)h * hd + d] = O * inv;
+    }
+}
+
+uint32_t attn_splits(uint32_t max_ctx, uint32_t n_kv)
+{
+    uint32_t a = (max_ctx + 15) / 16, b = (1024 + n_kv - 1) / n_kv;
+    uint32_t s = a < b ? a : b;
+    if (s < 1) s = 1;
+    if (s > 256) s = 256;
+    return s;
+}
+
+bool attn_supported(uint32_t hd, uint32_t group)
+{
+    bool e = hd == 32 || hd == 48 || hd == 64 || hd == 128;
+    bool g = group == 1 || group == 2 || group == 4 || group == 8;
+    return e && g;
+}
+
+template <int EPL>
+static hipError_t attn_g(uint32_t group, dim3 grid, hipStream_t s, const float *q, const float *kc,
+                         const float *vc, float *part, uint32_t n_kv, uint32_t ns, const StepState *st,
+                         uint32_t pos, float sc)
+{
+    switch (group) {
+    case 1: hipLaunchKernelGGL((k_attn<EPL, 1>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
+    case 2: hipLaunchKernelGGL((k_attn<EPL, 2>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
+    case 4: hipLaunchKernelGGL((k_attn<EPL, 4>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
+    case 8: hipLaunchKernelGGL((k_attn<EPL, 8>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const float *q, const float *kc, const float *vc, float *part, float *out,
+                            uint32_t n_head, uint32_t n_kv, uint32_t hd, uint32_t n_splits,
+                            const StepState *st, uint32_t pos_host, hipStream_t s)
+{
+    const uint32_t group = n_head / n_kv;
+    // scores are dot * (1/sqrtf(hd)) (attention.c:143,151-155), carried in log2 units
+    const float sc = (1.0f / sqrtf((float)hd)) * 1.4426950408889634f;
+    dim3 grid(n_kv * n_splits);
+    hipError_t e;
+    switch (hd) {
+    case 32: e = attn_g<2>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
+    case 48: e = attn_g<3>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
+    case 64: e = attn_g<4>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
+    case 128: e = attn_g<8>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(hd < 128 ? 64 : 128), 0, s, part, out, n_splits, hd);
+    return hipGetLastError();
+}
+
+// ── argmax (sampler_argmax, sampler.c:28-32) ─────────────────────────────────
+// Lowest index of the maximum; NaN never wins, and a NaN at index 0 makes the
+// answer 0 (the reference's strict '>' scan never leaves index 0 then).  One
+// launch: per-block partials, the last block to finish reduces them in order
+// and resets the ticket counter, so the kernel can be replayed in a graph.
+
+__device__ __forceinline__ bool am_better(float v1, uint32_t i1, float v2, uint32_t i2)
+{
+    if (i1 == 0xffffffffu) return false;
+    if (i2 == 0xffffffffu) return true;
+    return v1 > v2 || (v1 == v2 && i1 < i2);
+}
+
+__device__ void block_argmax(float &bv, uint32_t &bi)
+{
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        float ov = __shfl_xor(bv, m, 64);
+        uint32_t oi = __shfl_xor(bi, m, 64);
+        if (am_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (am_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    }
+}
+
+__device__ void greedy_advance(StepState *st, const uint32_t *prompt, uint32_t *ids, uint32_t next)
+{
+    const uint32_t pos = st->pos;
+    if (pos + 1 >= st->n_prompt) ids[pos + 1 - st->n_prompt] = next;
+    st->token = pos + 1 < st->n_prompt ? prompt[pos + 1] : next;
+    st->pos = pos + 1;
+}
+
+__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uint32_t n, float *pv,
+                                                 uint32_t *pi, uint32_t *counter, uint32_t *out, StepState *st,
+                                                 const uint32_t *prompt, uint32_t *ids)
+{
+    __shared__ bool s_last;
+    if (st && st->greedy && st->pos + 1 < st->n_prompt) {      // prefill step: logits unused
+        if (blockIdx.x == 0 && threadIdx.x == 0) greedy_advance(st, prompt, ids, 0);
+        return;
+    }
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float v = x[i];
+        if (!isnan(v) && (bi == 0xffffffffu || v > bv)) { bv = v; bi = i; }
+    }
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
+        __threadfence();
+        s_last = atomicAdd(counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    bv = -INFINITY;
+    bi = 0xffffffffu;
+    for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
+        float v = __builtin_nontemporal_load(pv + b);
+        uint32_t i = __builtin_nontemporal_load(pi + b);
+        if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) {
+        uint32_t r = (bi == 0xffffffffu || isnan(x[0])) ? 0u : bi;
+        *out = r;
+        *counter = 0u;
+        if (st) {
+            st->next = r;
+            if (st->greedy) greedy_advance(st, prompt, ids, r);
+        }
+    }
+}
+
+uint32_t argmax_blocks(uint32_t n)
+{
+    uint32_t b = (n + 2047) / 2048;
+    return b < 1 ? 1 : (b > 256 ? 256 : b);
+}
+
+hipError_t launch_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *counter, uint32_t *out,
+                         StepState *st, const uint32_t *prompt, uint32_t *ids, uint32_t n_blocks, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_argmax, dim3(n_blocks), dim3(256), 0, s, x, n, pv, pi, counter, out, st, prompt, ids);
+    return hipGetLastError();
+}
+
+// ── elementwise ──────────────────────────────────────────────────────────────
+
+__global__ void k_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t hd, const float *cos_tab,
+                       const float *sin_tab, int neox)
+{
+    const uint32_t half = hd / 2;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_heads * half) return;
+    const uint32_t h = i / half, p = i % half;
+    float *v = qk + (size_t)h * hd;
+    const uint32_t i0 = neox ? p : 2 * p, i1 = neox ? half + p : 2 * p + 1;
+    const float c = cos_tab[(size_t)pos * half + p], s = sin_tab[(size_t)pos * half + p];
+    const float v0 = v[i0], v1 = v[i1];
+    v[i0] = v0 * c - v1 * s;                         // rope.c:37-43 / 44-51
+    v[i1] = v0 * s + v1 * c;
+}
+
+hipError_t launch_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t hd, const float *cos_tab,
+                       const float *sin_tab, int neox, hipStream_t s)
+{
+    uint32_t n = n_heads * (hd / 2);
+    hipLaunchKernelGGL(k_rope, dim3((n + 255) / 256), dim3(256), 0, s, qk, pos, n_heads, hd, cos_tab, sin_tab, neox);
+    return hipGetLastError();
+}
+
+__global__ void k_silu_mul(const float *g, const float *u, float *out, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = silu_ref(g[i]) * u[i];
+}
+
+__global__ void k_silu(const float *x, float *out, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = silu_ref(x[i]);
+}
+
+__global__ void k_add(const float *a, const float *b, float *out, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = a[i] + b[i];
+}
+
+static uint32_t ew_blocks(uint64_t n)
+{
+    uint64_t b = (n + 255) / 256;
+    return (uint32_t)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_silu_mul, dim3(ew_blocks(n)), dim3(256), 0, s, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_silu, dim3(ew_blocks(n)), dim3(256), 0, s, x, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_add, dim3(ew_blocks(n)), dim3(256), 0, s, a, b, out, n);
+    return hipGetLastError();
+}
+
+} // namespace fw

@@ -1,0 +1,747 @@
+// forword_gpu_* C ABI: the per-token forward of forword.c on one MI355X.
+//
+// transformer_forward (transformer.c:149-326) becomes one token step queued on
+// the handle's stream: embedding row -> per layer [RMSNorm, fused QKV GEMV +
+// RoPE + KV append, split-K attention, Wo GEMV + residual, RMSNorm, fused
+// gate/up GEMV + SiLU*up, down GEMV + residual] -> RMSNorm -> lm-head GEMV ->
+// argmax.  The step reads token and position from a small device-resident
+// StepState, so it is captured once as a hipGraph and replayed for every
+// position; the greedy loop (main.c:145-217) replays it back to back with the
+// argmax kernel feeding the next token on the device.
+#include "fw_kernels.h"
+#include "forword_gpu.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <mutex>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+using namespace fw;
+
+static thread_local char g_err[512] = "";
+
+static void set_err(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "forword_gpu: %s\n", g_err);
+}
+
+#define HIPCHK(call, what)                                                               \
+    do {                                                                                 \
+        hipError_t e_ = (call);                                                          \
+        if (e_ != hipSuccess) {                                                          \
+            set_err("%s: %s", what, hipGetErrorString(e_));                              \
+            return -1;                                                                   \
+        }                                                                                \
+    } while (0)
+
+extern "C" const char *forword_gpu_last_error(void) { return g_err; }
+
+namespace {
+
+struct Lin {
+    const uint8_t *w = nullptr;
+    uint32_t type = 0, in = 0, out = 0;
+    uint64_t row_bytes = 0;
+};
+
+struct Layer {
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    Lin q, k, v, o, gate, up, down;
+};
+
+uint64_t type_row_bytes(uint32_t type, uint64_t cols)
+{
+    switch (type) {
+    case kF32: return cols * 4;
+    case kQ4_0: return cols / 32 * 18;
+    case kQ5_0: return cols / 32 * 22;
+    case kQ8_0: return cols / 32 * 34;
+    default: return 0;
+    }
+}
+
+} // namespace
+
+struct forword_gpu {
+    forword_gpu_config_t cfg{};
+    size_t n_ctx = 0;
+    hipStream_t stream = nullptr;
+    uint8_t *d_data = nullptr;
+    size_t data_size = 0;
+    Lin embd, out;
+    const float *out_norm = nullptr;
+    std::vector<Layer> L;
+    float *d_k = nullptr, *d_v = nullptr, *d_cos = nullptr, *d_sin = nullptr;
+    float *d_x = nullptr, *d_xn = nullptr, *d_q = nullptr, *d_att = nullptr, *d_h = nullptr;
+    float *d_logits = nullptr, *d_part = nullptr, *d_trace = nullptr, *d_pv = nullptr;
+    uint32_t *d_pi = nullptr, *d_counter = nullptr, *d_argmax = nullptr, *d_prompt = nullptr, *d_ids = nullptr;
+    StepState *d_state = nullptr, *h_state = nullptr;
+    float *h_logits = nullptr;
+    uint32_t *h_u32 = nullptr;
+    uint32_t n_splits = 1, am_blocks = 1;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool traced = false;
+    std::vector<void *> allocs;
+};
+
+static int dalloc(forword_gpu_t *h, void **p, size_t bytes, const char *what)
+{
+    hipError_t e = hipMalloc(p, bytes ? bytes : 4);
+    if (e != hipSuccess) {
+        set_err("hipMalloc(%zu) for %s: %s", bytes, what, hipGetErrorString(e));
+        return -1;
+    }
+    h->allocs.push_back(*p);
+    return 0;
+}
+
+static const forword_gpu_tensor_t *find_t(const forword_gpu_tensor_t *t, size_t n, const char *name)
+{
+    for (size_t i = 0; i < n; i++)
+        if (t[i].name && !strcmp(t[i].name, name)) return &t[i];
+    return nullptr;
+}
+
+// Bind a linear weight with its expected [in, out] shape (linear.c:169-170).
+static int bind_lin(forword_gpu_t *h, Lin &l, const forword_gpu_tensor_t *t, const char *name, uint64_t in,
+                    uint64_t out)
+{
+    if (!t) { set_err("missing tensor %s", name); return -1; }
+    if (t->ggml_type != kF32 && t->ggml_type != kQ4_0 && t->ggml_type != kQ5_0 && t->ggml_type != kQ8_0) {
+        set_err("tensor %s: unsupported ggml type %u", name, t->ggml_type);
+        return -1;
+    }
+    if (t->n_dims < 2 || t->dims[0] != in || t->dims[1] != out) {
+        set_err("tensor %s: shape [%llu, %llu], expected [%llu, %llu]", name, (unsigned long long)t->dims[0],
+                (unsigned long long)(t->n_dims > 1 ? t->dims[1] : 1), (unsigned long long)in,
+                (unsigned long long)out);
+        return -1;
+    }
+    if (t->ggml_type != kF32 && in % 32) { set_err("tensor %s: columns not a multiple of 32", name); return -1; }
+    uint64_t rb = type_row_bytes(t->ggml_type, in);
+    if (in >= (1u << 31) || out >= (1u << 31) || t->offset > h->data_size ||
+        rb * out > h->data_size - t->offset) {
+        set_err("tensor %s: data outside the data section", name);
+        return -1;
+    }
+    l.w = h->d_data + t->offset;
+    l.type = t->ggml_type;
+    l.in = (uint32_t)in;
+    l.out = (uint32_t)out;
+    l.row_bytes = rb;
+    return 0;
+}
+
+static int bind_vec(forword_gpu_t *h, const float **p, const forword_gpu_tensor_t *t, const char *name, uint64_t n,
+                    bool required)
+{
+    if (!t) {
+        if (required) { set_err("missing tensor %s", name); return -1; }
+        *p = nullptr;
+        return 0;
+    }
+    if (t->ggml_type != kF32 || t->offset > h->data_size || n * 4 > h->data_size - t->offset ||
+        (t->offset & 3)) {
+        set_err("tensor %s: expected %llu F32 values inside the data section", name, (unsigned long long)n);
+        return -1;
+    }
+    *p = reinterpret_cast<const float *>(h->d_data + t->offset);
+    return 0;
+}
+
+// ── one token step ───────────────────────────────────────────────────────────
+
+static hipError_t enqueue_step(forword_gpu_t *h)
+{
+    const forword_gpu_config_t &c = h->cfg;
+    const uint32_t n = c.n_embd, hd = c.head_dim, kvd = c.n_head_kv * hd;
+    hipStream_t s = h->stream;
+    hipError_t e;
+#define TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
+    TRY(launch_embed(h->embd.w, h->embd.type, n, h->embd.out, h->d_state, nullptr, c.embd_scale, h->d_x, s));
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const Layer &Ly = h->L[l];
+        float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
+        TRY(launch_rmsnorm(h->d_x, Ly.attn_norm, h->d_xn, n, c.norm_eps, s));          // transformer.c:261
+        // attention_forward (attention.c:124-140): Q/K/V, RoPE, KV append at pos
+        const Lin *qkv[3] = { &Ly.q, &Ly.k, &Ly.v };
+        const bool fused = Ly.q.type == Ly.k.type && Ly.k.type == Ly.v.type;
+        for (uint32_t s0 = 0; s0 < 3; s0 += fused ? 3 : 1) {
+            QmvArgs a{};
+            a.n_seg = fused ? 3 : 1;
+            for (uint32_t i = 0; i < a.n_seg; i++) { a.w[i] = qkv[s0 + i]->w; a.rows[i] = qkv[s0 + i]->out; }
+            a.role_base = s0;
+            a.n_cols = n;
+            a.row_bytes = qkv[s0]->row_bytes;
+            a.x = h->d_xn;
+            a.out[0] = h->d_q; a.out[1] = kc; a.out[2] = vc;
+            a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
+            a.state = h->d_state;
+            a.head_dim = hd;
+            a.kv_dim = kvd;
+            qmv_plan(a, EPI_QKV);
+            TRY(launch_qmv(qkv[s0]->type, EPI_QKV, a, s));
+        }
+        TRY(launch_attention(h->d_q, kc, vc, h->d_part, h->d_att, c.n_head, c.n_head_kv, hd, h->n_splits,
+                             h->d_state, 0, s));                                        // attention.c:142-164
+        {
+            QmvArgs a{};                                                                // attention.c:166 + transformer.c:271
+            a.n_seg = 1; a.w[0] = Ly.o.w; a.rows[0] = Ly.o.out; a.n_cols = Ly.o.in; a.row_bytes = Ly.o.row_bytes;
+            a.x = h->d_att; a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l) * n;
+            qmv_plan(a, EPI_RESID);
+            TRY(launch_qmv(Ly.o.type, EPI_RESID, a, s));
+        }
+        TRY(launch_rmsnorm(h->d_x, Ly.ffn_norm, h->d_xn, n, c.norm_eps, s));           // transformer.c:279
+        {
+            QmvArgs a{};                                                                // ffn.c:82-104
+            a.n_seg = 2; a.w[0] = Ly.gate.w; a.w[1] = Ly.up.w; a.rows[0] = a.rows[1] = c.n_ff;
+            a.n_cols = n; a.row_bytes = Ly.gate.row_bytes; a.x = h->d_xn; a.out[0] = h->d_h;
+            qmv_plan(a, EPI_SWIGLU);
+            TRY(launch_qmv(Ly.gate.type, EPI_SWIGLU, a, s));
+        }
+        {
+            QmvArgs a{};                                                                // ffn.c:106 + transformer.c:287
+            a.n_seg = 1; a.w[0] = Ly.down.w; a.rows[0] = n; a.n_cols = c.n_ff; a.row_bytes = Ly.down.row_bytes;
+            a.x = h->d_h; a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l + 1) * n;
+            qmv_plan(a, EPI_RESID);
+            TRY(launch_qmv(Ly.down.type, EPI_RESID, a, s));
+        }
+    }
+    if (h->out_norm) TRY(launch_rmsnorm(h->d_x, h->out_norm, h->d_xn, n, c.norm_eps, s));  // transformer.c:293-304
+    else TRY(hipMemcpyAsync(h->d_xn, h->d_x, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+    {
+        QmvArgs a{};                                                                    // transformer.c:310-323
+        a.n_seg = 1; a.w[0] = h->out.w; a.rows[0] = h->out.out; a.n_cols = n; a.row_bytes = h->out.row_bytes;
+        a.x = h->d_xn; a.out[0] = h->d_logits; a.state = h->d_state;
+        qmv_plan(a, EPI_STORE);
+        TRY(launch_qmv(h->out.type, EPI_STORE, a, s));
+    }
+    TRY(launch_argmax(h->d_logits, c.n_vocab, h->d_pv, h->d_pi, h->d_counter, h->d_argmax, h->d_state, h->d_prompt,
+                      h->d_ids, h->am_blocks, s));
+#undef TRY
+    return hipSuccess;
+}
+
+static int run_step(forword_gpu_t *h)
+{
+    if (h->exec) HIPCHK(hipGraphLaunch(h->exec, h->stream), "hipGraphLaunch");
+    else HIPCHK(enqueue_step(h), "token step launch");
+    return 0;
+}
+
+static void build_graph(forword_gpu_t *h)
+{
+    const char *env = getenv("FORWORD_GPU_GRAPH");
+    if (env && !strcmp(env, "0")) return;
+    if (hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return;
+    hipError_t e = enqueue_step(h);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(h->stream, &g);
+    if (e != hipSuccess || e2 != hipSuccess || !g) {
+        if (g) (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        fprintf(stderr, "forword_gpu: graph capture failed (%s); launching kernels directly\n",
+                hipGetErrorString(e != hipSuccess ? e : e2));
+        return;
+    }
+    if (hipGraphInstantiate(&h->exec, g, nullptr, nullptr, 0) != hipSuccess) {
+        h->exec = nullptr;
+        (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        fprintf(stderr, "forword_gpu: graph instantiation failed; launching kernels directly\n");
+        return;
+    }
+    h->graph = g;
+}
+
+// ── model-level ABI ──────────────────────────────────────────────────────────
+
+extern "C" void forword_gpu_free(forword_gpu_t *h)
+{
+    if (!h) return;
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->exec) (void)hipGraphExecDestroy(h->exec);
+    if (h->graph) (void)hipGraphDestroy(h->graph);
+    for (void *p : h->allocs) (void)hipFree(p);
+    if (h->h_state) (void)hipHostFree(h->h_state);
+    if (h->h_logits) (void)hipHostFree(h->h_logits);
+    if (h->h_u32) (void)hipHostFree(h->h_u32);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t data_size,
+                                const forword_gpu_tensor_t *tensors, size_t n_tensors,
+                                const forword_gpu_config_t *cfg, size_t max_ctx, const float *cos_tab,
+                                const float *sin_tab)
+{
+    if (!out) { set_err("forword_gpu_init: out is NULL"); return -1; }
+    *out = nullptr;
+    if (!data || !data_size || !tensors || !cfg || !cos_tab || !sin_tab || !max_ctx) {
+        set_err("forword_gpu_init: invalid arguments");
+        return -1;
+    }
+    const forword_gpu_config_t &c = *cfg;
+    if (!c.n_embd || !c.n_head || !c.n_layer || !c.n_vocab || !c.n_ff || !c.n_head_kv ||
+        c.n_head % c.n_head_kv || c.head_dim * c.n_head != c.n_embd || c.n_embd % 32 || c.n_ff % 32) {
+        set_err("forword_gpu_init: invalid model dimensions");
+        return -1;
+    }
+    if (c.norm_type != FORWORD_NORM_RMS || c.act_type != FORWORD_ACT_SILU || !c.use_ffn_gate ||
+        c.use_qkv_bias || c.parallel_res || c.rope_type != FORWORD_ROPE_NORMAL) {
+        set_err("forword_gpu_init: only the llama block (RMSNorm, SwiGLU, RoPE pairs (2i,2i+1), no biases, "
+                "sequential residual) is implemented");
+        return -1;
+    }
+    if (!attn_supported(c.head_dim, c.n_head / c.n_head_kv)) {
+        set_err("forword_gpu_init: head_dim %u / GQA group %u not supported by the attention kernel",
+                c.head_dim, c.n_head / c.n_head_kv);
+        return -1;
+    }
+    if (max_ctx > c.n_ctx || max_ctx >= (1u << 31)) {
+        set_err("forword_gpu_init: max_ctx %zu exceeds the model context %u", max_ctx, c.n_ctx);
+        return -1;
+    }
+
+    forword_gpu_t *h = new forword_gpu_t();
+    h->cfg = c;
+    h->n_ctx = max_ctx;
+    h->data_size = data_size;
+    const uint32_t n = c.n_embd, hd = c.head_dim, kvd = c.n_head_kv * hd;
+#define FAIL() do { forword_gpu_free(h); return -1; } while (0)
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+        set_err("hipStreamCreate failed");
+        FAIL();
+    }
+    if (dalloc(h, (void **)&h->d_data, data_size, "weights")) FAIL();
+    if (hipMemcpy(h->d_data, data, data_size, hipMemcpyHostToDevice) != hipSuccess) {
+        set_err("weight upload failed");
+        FAIL();
+    }
+
+    // resolve every tensor once (tensor_find, tensor_data.c:8-23)
+    const forword_gpu_tensor_t *te = find_t(tensors, n_tensors, "token_embd.weight");
+    const forword_gpu_tensor_t *to = find_t(tensors, n_tensors, "output.weight");
+    if (!to) to = find_t(tensors, n_tensors, "lm_head.weight");
+    if (!to) to = te;                                                                   // transformer.c:310-316
+    if (bind_lin(h, h->embd, te, "token_embd.weight", n, c.n_vocab)) FAIL();
+    if (bind_lin(h, h->out, to, "output.weight", n, c.n_vocab)) FAIL();
+    if (bind_vec(h, &h->out_norm, find_t(tensors, n_tensors, "output_norm.weight"), "output_norm.weight", n, false))
+        FAIL();
+    h->L.resize(c.n_layer);
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        char nm[96];
+        Layer &Ly = h->L[l];
+#define LIN(f, sfx, in_, out_)                                                          \
+        snprintf(nm, sizeof nm, "blk.%u." sfx, l);                                      \
+        if (bind_lin(h, Ly.f, find_t(tensors, n_tensors, nm), nm, in_, out_)) FAIL();
+        LIN(q, "attn_q.weight", n, n);
+        LIN(k, "attn_k.weight", n, kvd);
+        LIN(v, "attn_v.weight", n, kvd);
+        LIN(o, "attn_output.weight", n, n);
+        LIN(gate, "ffn_gate.weight", n, c.n_ff);
+        LIN(up, "ffn_up.weight", n, c.n_ff);
+        LIN(down, "ffn_down.weight", c.n_ff, n);
+#undef LIN
+        if (Ly.gate.type != Ly.up.type) { set_err("layer %u: ffn_gate and ffn_up types differ", l); FAIL(); }
+        snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l);
+        if (bind_vec(h, &Ly.attn_norm, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
+        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);
+        if (bind_vec(h, &Ly.ffn_norm, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
+    }
+
+    const size_t kv_elems = (size_t)c.n_layer * max_ctx * kvd, half = hd / 2;
+    h->n_splits = attn_splits((uint32_t)max_ctx, c.n_head_kv);
+    h->am_blocks = argmax_blocks(c.n_vocab);
+    if (dalloc(h, (void **)&h->d_k, kv_elems * 4, "K cache") || dalloc(h, (void **)&h->d_v, kv_elems * 4, "V cache") ||
+        dalloc(h, (void **)&h->d_cos, max_ctx * half * 4, "RoPE cos") ||
+        dalloc(h, (void **)&h->d_sin, max_ctx * half * 4, "RoPE sin") ||
+        dalloc(h, (void **)&h->d_x, (size_t)n * 4, "x") || dalloc(h, (void **)&h->d_xn, (size_t)n * 4, "xn") ||
+        dalloc(h, (void **)&h->d_q, (size_t)n * 4, "q") || dalloc(h, (void **)&h->d_att, (size_t)n * 4, "attn") ||
+        dalloc(h, (void **)&h->d_h, (size_t)c.n_ff * 4, "ffn") ||
+        dalloc(h, (void **)&h->d_logits, (size_t)c.n_vocab * 4, "logits") ||
+        dalloc(h, (void **)&h->d_part, (size_t)c.n_head * h->n_splits * (hd + 2) * 4, "attention partials") ||
+        dalloc(h, (void **)&h->d_trace, (size_t)2 * c.n_layer * n * 4, "trace") ||
+        dalloc(h, (void **)&h->d_pv, h->am_blocks * 4, "argmax") || dalloc(h, (void **)&h->d_pi, h->am_blocks * 4, "argmax") ||
+        dalloc(h, (void **)&h->d_counter, 4, "argmax") || dalloc(h, (void **)&h->d_argmax, 4, "argmax") ||
+        dalloc(h, (void **)&h->d_prompt, max_ctx * 4, "prompt") || dalloc(h, (void **)&h->d_ids, (max_ctx + 1) * 4, "ids") ||
+        dalloc(h, (void **)&h->d_state, sizeof(StepState), "state"))
+        FAIL();
+    if (hipHostMalloc((void **)&h->h_state, sizeof(StepState), 0) != hipSuccess ||
+        hipHostMalloc((void **)&h->h_logits, (size_t)c.n_vocab * 4, 0) != hipSuccess ||
+        hipHostMalloc((void **)&h->h_u32, 4 * 4, 0) != hipSuccess) {
+        set_err("pinned host allocation failed");
+        FAIL();
+    }
+    memset(h->h_state, 0, sizeof(StepState));
+    if (hipMemset(h->d_k, 0, kv_elems * 4) != hipSuccess || hipMemset(h->d_v, 0, kv_elems * 4) != hipSuccess ||
+        hipMemset(h->d_counter, 0, 4) != hipSuccess || hipMemset(h->d_state, 0, sizeof(StepState)) != hipSuccess ||
+        hipMemset(h->d_trace, 0, (size_t)2 * c.n_layer * n * 4) != hipSuccess ||
+        hipMemcpy(h->d_cos, cos_tab, max_ctx * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(h->d_sin, sin_tab, max_ctx * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        set_err("device initialisation failed");
+        FAIL();
+    }
+    build_graph(h);
+#undef FAIL
+    *out = h;
+    return 0;
+}
+
+static int check_tok_pos(forword_gpu_t *h, uint32_t token, size_t pos)
+{
+    if (!h) { set_err("NULL handle"); return -1; }
+    if (pos >= h->n_ctx) { set_err("position %zu exceeds KV cache (%zu)", pos, h->n_ctx); return -1; }
+    if (token >= h->cfg.n_vocab) { set_err("token ID %u out of range", token); return -1; }
+    return 0;
+}
+
+static int step_once(forword_gpu_t *h, uint32_t token, size_t pos)
+{
+    // a host-driven step ends any device-resident greedy loop
+    h->h_state->token = token;
+    h->h_state->pos = (uint32_t)pos;
+    h->h_state->n_prompt = 0;
+    h->h_state->greedy = 0;
+    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    if (run_step(h)) return -1;
+    h->traced = true;
+    return 0;
+}
+
+extern "C" float *forword_gpu_forward(forword_gpu_t *h, uint32_t token_id, size_t pos)
+{
+    if (check_tok_pos(h, token_id, pos) || step_once(h, token_id, pos)) return nullptr;
+    if (hipMemcpyAsync(h->h_logits, h->d_logits, (size_t)h->cfg.n_vocab * 4, hipMemcpyDeviceToHost, h->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(h->stream) != hipSuccess) {
+        set_err("forward: %s", hipGetErrorString(hipGetLastError()));
+        return nullptr;
+    }
+    return h->h_logits;
+}
+
+extern "C" int forword_gpu_forward_argmax(forword_gpu_t *h, uint32_t token_id, size_t pos, uint32_t *next)
+{
+    if (!next) { set_err("forward_argmax: next is NULL"); return -1; }
+    if (check_tok_pos(h, token_id, pos) || step_once(h, token_id, pos)) return -1;
+    HIPCHK(hipMemcpyAsync(h->h_u32, h->d_argmax, 4, hipMemcpyDeviceToHost, h->stream), "argmax download");
+    HIPCHK(hipStreamSynchronize(h->stream), "forward_argmax");
+    *next = h->h_u32[0];
+    return 0;
+}
+
+extern "C" int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                                           uint32_t *out_ids)
+{
+    if (!h || !prompt || !n_prompt || (n_gen && !out_ids)) { set_err("generate_greedy: invalid arguments"); return -1; }
+    const size_t n_fwd = n_gen ? n_prompt + n_gen - 1 : n_prompt;
+    if (n_fwd > h->n_ctx) { set_err("generate_greedy: %zu forwards exceed the KV cache (%zu)", n_fwd, h->n_ctx); return -1; }
+    for (size_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= h->cfg.n_vocab) { set_err("generate_greedy: prompt token %u out of range", prompt[i]); return -1; }
+    HIPCHK(hipMemcpyAsync(h->d_prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice, h->stream), "prompt upload");
+    h->h_state->token = prompt[0];
+    h->h_state->pos = 0;
+    h->h_state->n_prompt = (uint32_t)n_prompt;
+    h->h_state->next = 0;
+    h->h_state->greedy = 1;
+    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    for (size_t f = 0; f < n_fwd; f++)
+        if (run_step(h)) return -1;
+    if (n_gen) HIPCHK(hipMemcpyAsync(out_ids, h->d_ids, n_gen * 4, hipMemcpyDeviceToHost, h->stream), "ids download");
+    HIPCHK(hipStreamSynchronize(h->stream), "generate_greedy");
+    h->h_state->pos = (uint32_t)n_fwd;     // host mirror of the device state, for forword_gpu_decode
+    h->traced = true;
+    return 0;
+}
+
+extern "C" int forword_gpu_decode(forword_gpu_t *h, size_t n_steps, uint32_t *out_ids)
+{
+    if (!h) { set_err("decode: NULL handle"); return -1; }
+    if (!h->h_state->greedy) { set_err("decode: no greedy loop to continue (call generate_greedy first)"); return -1; }
+    const size_t pos = h->h_state->pos, n_prompt = h->h_state->n_prompt;
+    if (pos + n_steps > h->n_ctx) { set_err("decode: %zu more forwards exceed the KV cache (%zu)", n_steps, h->n_ctx); return -1; }
+    for (size_t i = 0; i < n_steps; i++)
+        if (run_step(h)) return -1;
+    h->h_state->pos = (uint32_t)(pos + n_steps);
+    if (out_ids && n_steps) {
+        // step at position p writes the token for position p+1 at ids[p + 1 - n_prompt]
+        HIPCHK(hipMemcpyAsync(out_ids, h->d_ids + (pos + 1 - n_prompt), n_steps * 4, hipMemcpyDeviceToHost, h->stream),
+               "ids download");
+        HIPCHK(hipStreamSynchronize(h->stream), "decode");
+    }
+    return 0;
+}
+
+static int kv_args(forword_gpu_t *h, size_t layer, size_t pos0, size_t n_pos)
+{
+    if (!h) { set_err("NULL handle"); return -1; }
+    if (layer >= h->cfg.n_layer || pos0 > h->n_ctx || n_pos > h->n_ctx - pos0) {
+        set_err("kv: layer %zu / positions [%zu, %zu) out of range", layer, pos0, pos0 + n_pos);
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" int forword_gpu_kv_write(forword_gpu_t *h, size_t layer, size_t pos0, size_t n_pos, const float *k,
+                                    const float *v)
+{
+    if (kv_args(h, layer, pos0, n_pos)) return -1;
+    const size_t kvd = (size_t)h->cfg.n_head_kv * h->cfg.head_dim, off = (layer * h->n_ctx + pos0) * kvd;
+    HIPCHK(hipStreamSynchronize(h->stream), "kv_write");
+    if (k) HIPCHK(hipMemcpy(h->d_k + off, k, n_pos * kvd * 4, hipMemcpyHostToDevice), "kv_write K");
+    if (v) HIPCHK(hipMemcpy(h->d_v + off, v, n_pos * kvd * 4, hipMemcpyHostToDevice), "kv_write V");
+    return 0;
+}
+
+extern "C" int forword_gpu_kv_read(forword_gpu_t *h, size_t layer, size_t pos0, size_t n_pos, float *k, float *v)
+{
+    if (kv_args(h, layer, pos0, n_pos)) return -1;
+    const size_t kvd = (size_t)h->cfg.n_head_kv * h->cfg.head_dim, off = (layer * h->n_ctx + pos0) * kvd;
+    HIPCHK(hipStreamSynchronize(h->stream), "kv_read");
+    if (k) HIPCHK(hipMemcpy(k, h->d_k + off, n_pos * kvd * 4, hipMemcpyDeviceToHost), "kv_read K");
+    if (v) HIPCHK(hipMemcpy(v, h->d_v + off, n_pos * kvd * 4, hipMemcpyDeviceToHost), "kv_read V");
+    return 0;
+}
+
+extern "C" int forword_gpu_layer_trace(forword_gpu_t *h, float *out)
+{
+    if (!h || !out) { set_err("layer_trace: invalid arguments"); return -1; }
+    if (!h->traced) { set_err("layer_trace: no forward has run yet"); return -1; }
+    HIPCHK(hipStreamSynchronize(h->stream), "layer_trace");
+    HIPCHK(hipMemcpy(out, h->d_trace, (size_t)2 * h->cfg.n_layer * h->cfg.n_embd * 4, hipMemcpyDeviceToHost),
+           "layer_trace");
+    return 0;
+}
+
+extern "C" size_t forword_gpu_n_ctx(const forword_gpu_t *h) { return h ? h->n_ctx : 0; }
+extern "C" void *forword_gpu_stream(const forword_gpu_t *h) { return h ? (void *)h->stream : nullptr; }
+
+// ── operator level ───────────────────────────────────────────────────────────
+
+namespace {
+// Scratch shared by operator-level calls on this device: argmax partials and
+// attention partials.  Calls that overlap on different streams race on it.
+std::mutex g_scratch_mu;
+float *g_pv = nullptr;
+uint32_t *g_pi = nullptr, *g_counter = nullptr;
+float *g_part = nullptr;
+size_t g_part_bytes = 0;
+
+int op_scratch_argmax()
+{
+    if (g_counter) return 0;
+    if (hipMalloc(&g_pv, 256 * 4) != hipSuccess || hipMalloc(&g_pi, 256 * 4) != hipSuccess ||
+        hipMalloc(&g_counter, 4) != hipSuccess || hipMemset(g_counter, 0, 4) != hipSuccess) {
+        set_err("argmax scratch allocation failed");
+        return -1;
+    }
+    return 0;
+}
+
+int op_scratch_part(size_t bytes)
+{
+    if (g_part_bytes >= bytes) return 0;
+    if (g_part) { (void)hipDeviceSynchronize(); (void)hipFree(g_part); g_part = nullptr; g_part_bytes = 0; }
+    if (hipMalloc(&g_part, bytes) != hipSuccess) { set_err("attention scratch allocation failed"); return -1; }
+    g_part_bytes = bytes;
+    return 0;
+}
+
+int launched(hipError_t e, const char *what)
+{
+    if (e != hipSuccess) { set_err("%s: %s", what, hipGetErrorString(e)); return -1; }
+    return 0;
+}
+} // namespace
+
+extern "C" int forword_gpu_quant_matvec(const void *weights, size_t weights_size, uint32_t type, const float *input,
+                                        float *output, size_t in, size_t out, void *stream)
+{
+    if (!weights || !input || !output || !in || !out) { set_err("quant_matvec: invalid arguments"); return -1; }
+    uint64_t rb;
+    if (type == kF32) rb = (uint64_t)in * 4;
+    else if (type == kQ4_0 || type == kQ5_0 || type == kQ8_0) {
+        if (in % 32) { set_err("quant_matvec: input size not a multiple of 32"); return -1; }
+        rb = type_row_bytes(type, in);
+    } else { set_err("quant_matvec: unsupported ggml type %u", type); return -1; }
+    if (in >= (1u << 31) || out >= (1u << 31) || out > SIZE_MAX / rb || weights_size < out * rb) {
+        set_err("quant_matvec: weights buffer too small or sizes too large");
+        return -1;
+    }
+    QmvArgs a{};
+    a.n_seg = 1; a.w[0] = (const uint8_t *)weights; a.rows[0] = (uint32_t)out; a.n_cols = (uint32_t)in;
+    a.row_bytes = rb; a.x = input; a.out[0] = output;
+    qmv_plan(a, EPI_STORE);
+    return launched(launch_qmv(type, EPI_STORE, a, (hipStream_t)stream), "quant_matvec");
+}
+
+extern "C" int forword_gpu_ffn_swiglu(const void *w_gate, const void *w_up, size_t weights_size, uint32_t type,
+                                      const float *x, float *hout, size_t in, size_t n_ff, void *stream)
+{
+    if (!w_gate || !w_up || !x || !hout || !in || !n_ff) { set_err("ffn_swiglu: invalid arguments"); return -1; }
+    if ((type != kQ4_0 && type != kQ5_0 && type != kQ8_0 && type != kF32) || (type != kF32 && in % 32)) {
+        set_err("ffn_swiglu: unsupported type or input size");
+        return -1;
+    }
+    uint64_t rb = type_row_bytes(type, in);
+    if (in >= (1u << 31) || n_ff >= (1u << 31) || weights_size < n_ff * rb) {
+        set_err("ffn_swiglu: weights buffer too small or sizes too large");
+        return -1;
+    }
+    QmvArgs a{};
+    a.n_seg = 2; a.w[0] = (const uint8_t *)w_gate; a.w[1] = (const uint8_t *)w_up;
+    a.rows[0] = a.rows[1] = (uint32_t)n_ff; a.n_cols = (uint32_t)in; a.row_bytes = rb; a.x = x; a.out[0] = hout;
+    qmv_plan(a, EPI_SWIGLU);
+    return launched(launch_qmv(type, EPI_SWIGLU, a, (hipStream_t)stream), "ffn_swiglu");
+}
+
+extern "C" int forword_gpu_tensor_matvec_f32(const float *weights, const float *x, float *y, size_t rows,
+                                             size_t cols, void *stream)
+{
+    if (!weights || !x || !y || !rows || !cols) { set_err("tensor_matvec_f32: invalid arguments"); return -1; }
+    return forword_gpu_quant_matvec(weights, rows * cols * 4, kF32, x, y, cols, rows, stream);
+}
+
+extern "C" int forword_gpu_dequant(const void *blocks, size_t size, uint32_t type, float *out, size_t count,
+                                   void *stream)
+{
+    uint64_t bb = type_row_bytes(type, 32);
+    if (!blocks || !out || type == kF32 || !bb || !size || size % bb || count % 32 || size / bb != count / 32) {
+        set_err("dequant: invalid arguments");
+        return -1;
+    }
+    return launched(launch_dequant((const uint8_t *)blocks, type, size / bb, out, (hipStream_t)stream), "dequant");
+}
+
+extern "C" int forword_gpu_get_row(const void *w, size_t size, uint32_t type, size_t n_cols, size_t row, float *out,
+                                   void *stream)
+{
+    if (!w || !out || !n_cols || n_cols >= (1u << 31) || row >= (1u << 31)) { set_err("get_row: invalid arguments"); return -1; }
+    if (type != kF32 && (type_row_bytes(type, 32) == 0 || n_cols % 32)) { set_err("get_row: unsupported type or shape"); return -1; }
+    uint64_t rb = type_row_bytes(type, n_cols);
+    if (rb == 0 || (row + 1) > size / rb) { set_err("get_row: row outside the tensor"); return -1; }
+    return launched(launch_get_row((const uint8_t *)w, type, (uint32_t)n_cols, (uint32_t)row, out, (hipStream_t)stream),
+                    "get_row");
+}
+
+extern "C" int forword_gpu_rms_norm(const float *x, const float *w, float *out, size_t n, float eps, void *stream)
+{
+    if (!x || !out || n >= (1u << 31)) { set_err("rms_norm: invalid arguments"); return -1; }
+    if (!n) return 0;
+    return launched(launch_rmsnorm(x, w, out, (uint32_t)n, eps, (hipStream_t)stream), "rms_norm");
+}
+
+extern "C" int forword_gpu_tensor_rms_norm(const float *x, const float *w, float *out, size_t n, float eps, void *stream)
+{
+    if (!x || !w || !out || !n || !isfinite(eps) || eps <= 0.0f) { set_err("tensor_rms_norm: invalid arguments"); return -1; }
+    return forword_gpu_rms_norm(x, w, out, n, eps, stream);
+}
+
+extern "C" int forword_gpu_rope_apply(float *qk, size_t pos, size_t n_heads, size_t hd, const float *cos_tab,
+                                      const float *sin_tab, int neox, void *stream)
+{
+    if (!qk || !cos_tab || !sin_tab || !hd || hd % 2 || n_heads * hd >= (1u << 31) || pos >= (1u << 31)) {
+        set_err("rope_apply: invalid arguments");
+        return -1;
+    }
+    if (!n_heads) return 0;
+    return launched(launch_rope(qk, (uint32_t)pos, (uint32_t)n_heads, (uint32_t)hd, cos_tab, sin_tab, neox,
+                                (hipStream_t)stream), "rope_apply");
+}
+
+extern "C" int forword_gpu_attention(const float *q, const float *kc, const float *vc, float *out, size_t n_head,
+                                     size_t n_kv, size_t hd, size_t n_ctx, size_t pos, void *stream)
+{
+    if (!q || !kc || !vc || !out || !n_head || !n_kv || !hd || n_head % n_kv || pos >= n_ctx || n_ctx >= (1u << 31)) {
+        set_err("attention: invalid head configuration or position");
+        return -1;
+    }
+    if (!attn_supported((uint32_t)hd, (uint32_t)(n_head / n_kv))) {
+        set_err("attention: head_dim %zu / GQA group %zu not supported", hd, n_head / n_kv);
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    const uint32_t ns = attn_splits((uint32_t)(pos + 1), (uint32_t)n_kv);
+    if (op_scratch_part((size_t)n_head * ns * (hd + 2) * 4)) return -1;
+    return launched(launch_attention(q, kc, vc, g_part, out, (uint32_t)n_head, (uint32_t)n_kv, (uint32_t)hd, ns, nullptr,
+                                     (uint32_t)pos, (hipStream_t)stream), "attention");
+}
+
+extern "C" int forword_gpu_silu_mul(const float *g, const float *u, float *out, size_t n, void *stream)
+{
+    if (!g || !u || !out) { set_err("silu_mul: invalid arguments"); return -1; }
+    if (!n) return 0;
+    return launched(launch_silu_mul(g, u, out, n, (hipStream_t)stream), "silu_mul");
+}
+
+extern "C" int forword_gpu_tensor_silu(const float *x, float *out, size_t n, void *stream)
+{
+    if (!x || !out || !n) { set_err("tensor_silu: invalid arguments"); return -1; }
+    return launched(launch_silu(x, out, n, (hipStream_t)stream), "tensor_silu");
+}
+
+extern "C" int forword_gpu_tensor_add(const float *a, const float *b, float *out, size_t n, void *stream)
+{
+    if (!a || !b || !out || !n) { set_err("tensor_add: invalid arguments"); return -1; }
+    return launched(launch_add(a, b, out, n, (hipStream_t)stream), "tensor_add");
+}
+
+extern "C" int forword_gpu_argmax(const float *logits, size_t n, uint32_t *out_index, void *stream)
+{
+    if (!logits || !out_index || n >= (1u << 31)) { set_err("argmax: invalid arguments"); return -1; }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (op_scratch_argmax()) return -1;
+    return launched(launch_argmax(logits, (uint32_t)n, g_pv, g_pi, g_counter, out_index, nullptr, nullptr, nullptr,
+                                  argmax_blocks((uint32_t)n), (hipStream_t)stream), "argmax");
+}
+
+// ── device memory plumbing ───────────────────────────────────────────────────
+
+extern "C" void *forword_gpu_dev_alloc(size_t bytes)
+{
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) { set_err("hipMalloc(%zu) failed", bytes); return nullptr; }
+    return p;
+}
+
+extern "C" int forword_gpu_dev_free(void *p)
+{
+    if (p) HIPCHK(hipFree(p), "hipFree");
+    return 0;
+}
+
+extern "C" int forword_gpu_memcpy_h2d(void *dst, const void *src, size_t n)
+{
+    HIPCHK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice), "memcpy_h2d");
+    return 0;
+}
+
+extern "C" int forword_gpu_memcpy_d2h(void *dst, const void *src, size_t n)
+{
+    HIPCHK(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost), "memcpy_d2h");
+    return 0;
+}
+
+extern "C" int forword_gpu_memset(void *dst, int v, size_t n)
+{
+    HIPCHK(hipMemset(dst, v, n), "memset");
+    return 0;
+}
+
+extern "C" int forword_gpu_synchronize(void *stream)
+{
+    if (stream) HIPCHK(hipStreamSynchronize((hipStream_t)stream), "synchronize");
+    else HIPCHK(hipDeviceSynchronize(), "synchronize");
+    return 0;
+}

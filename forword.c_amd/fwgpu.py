@@ -150,6 +150,8 @@ def gpu_lib():
         _sig(L, "forword_gpu_forward", fp, [vp, u32, sz])
         _sig(L, "forword_gpu_forward_argmax", C.c_int, [vp, u32, sz, u32p])
         _sig(L, "forword_gpu_generate_greedy", C.c_int, [vp, u32p, sz, sz, u32p])
+        _sig(L, "forword_gpu_decode", C.c_int, [vp, sz, u32p])
+        _sig(L, "forword_gpu_ffn_swiglu", C.c_int, [vp, vp, sz, u32, vp, vp, sz, sz, vp])
         _sig(L, "forword_gpu_kv_write", C.c_int, [vp, sz, sz, sz, fp, fp])
         _sig(L, "forword_gpu_kv_read", C.c_int, [vp, sz, sz, sz, fp, fp])
         _sig(L, "forword_gpu_layer_trace", C.c_int, [vp, fp])
@@ -334,6 +336,13 @@ class GpuModel:
                                                      out.ctypes.data_as(u32p)), "generate_greedy")
         return out
 
+    def decode(self, n_steps: int, copy_out: bool = True):
+        """Continue the device-resident greedy loop; without copy_out only queue the steps."""
+        out = np.zeros(n_steps, np.uint32) if copy_out else None
+        _check(gpu_lib().forword_gpu_decode(self.h, n_steps, out.ctypes.data_as(u32p) if copy_out else None),
+               "decode")
+        return out
+
     def kv_write(self, layer: int, pos0: int, k: np.ndarray | None, v: np.ndarray | None):
         k = None if k is None else np.ascontiguousarray(k, np.float32)
         v = None if v is None else np.ascontiguousarray(v, np.float32)
@@ -448,6 +457,15 @@ class ops:
     @staticmethod
     def silu_mul(gate, up, out, n):
         ops._sync(gpu_lib().forword_gpu_silu_mul(gate.ptr, up.ptr, out.ptr, n, None), "silu_mul")
+
+    @staticmethod
+    def ffn_swiglu(w_gate, w_up, ggml_type, x, h, n_in, n_ff, stream=None, sync=True):
+        rc = gpu_lib().forword_gpu_ffn_swiglu(w_gate.ptr, w_up.ptr, min(w_gate.nbytes, w_up.nbytes), ggml_type,
+                                              x.ptr, h.ptr, n_in, n_ff, stream)
+        if sync:
+            ops._sync(rc, "ffn_swiglu")
+        else:
+            _check(rc, "ffn_swiglu")
 
     @staticmethod
     def tensor_matvec_f32(w, x, y, rows, cols):

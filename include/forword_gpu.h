@@ -120,6 +120,15 @@ int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *prompt, size_t
                                 size_t n_gen, uint32_t *out_ids);
 
 /*
+ * Continue the greedy loop of the last forword_gpu_generate_greedy for n_steps
+ * more forwards, each fed the previous argmax (main.c:173-217, decode part).
+ * With out_ids != NULL the n_steps new tokens are copied out and the call
+ * waits; with out_ids == NULL the steps are only queued on the handle's stream
+ * (for timing with stream events) and the call returns at once.
+ */
+int forword_gpu_decode(forword_gpu_t *h, size_t n_steps, uint32_t *out_ids);
+
+/*
  * Write / read rows of the device KV cache for one layer: positions
  * [pos0, pos0+n_pos), each row n_head_kv*head_dim floats, K post-RoPE
  * (kv_k/kv_v, kv_cache.h:45-51; the append in attention.c:135-140).
@@ -190,6 +199,12 @@ int forword_gpu_attention(const float *q, const float *k_cache, const float *v_c
 
 /* out = silu(gate) * up, n elements (ffn.c:88-91,103-104 with apply_silu ffn.c:17-25). */
 int forword_gpu_silu_mul(const float *gate, const float *up, float *out, size_t n, void *stream);
+
+/* h[n_ff] = silu(W_gate . x) * (W_up . x), the gated FFN up to the down
+ * projection (ffn.c:82-104) as one fused GEMV; both weights of one ggml type,
+ * [n_ff][n_in] each. */
+int forword_gpu_ffn_swiglu(const void *w_gate, const void *w_up, size_t weights_size, uint32_t ggml_type,
+                           const float *x, float *h, size_t n_in, size_t n_ff, void *stream);
 
 /* tensor_ops.c counterparts (tensor_ops.h:6-33). */
 int forword_gpu_tensor_matvec_f32(const float *weights, const float *x, float *y,
