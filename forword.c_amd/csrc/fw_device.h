@@ -203,6 +203,35 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+// Cross-workgroup communication without cache maintenance.  The L2 of each of
+// the eight XCDs is not coherent with the others, and an agent-scope release
+// fence writes the whole L2 back (~10 us for 256 workgroups).  Values one
+// workgroup publishes for another therefore go through system-scope relaxed
+// atomics (sc0 sc1: written through / read past the L2), ordered by an
+// explicit wait for this wave's outstanding memory operations.
+__device__ __forceinline__ void st_sys(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_sys(uint32_t *p, uint32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float ld_sys(const float *p)
+{
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint32_t ld_sys(const uint32_t *p)
+{
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint32_t ticket_sys(uint32_t *p)
+{
+    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0): every memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
 // expf through double precision: the float result is the correctly rounded
 // e^v except where the double lands within an ulp of a float rounding midpoint.
 __device__ __forceinline__ float exp_f32(float v) { return (float)exp((double)v); }

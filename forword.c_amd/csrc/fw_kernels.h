@@ -42,6 +42,17 @@ struct QmvArgs {
     const StepState *state;
     uint32_t head_dim;
     uint32_t kv_dim;           // n_head_kv * head_dim (K/V cache row length)
+    // Input RMSNorm folded into the load of x (norm.c:7-16): x_j -> (x_j*norm_w[j])*scale,
+    // scale read from *norm_scale.  Off when norm_w is null.
+    const float *norm_w;
+    const float *norm_scale;
+    // RESID only: publish 1/sqrt(mean(x_new^2)+eps) of the updated residual for the
+    // next RMSNorm (off when scale_out is null): per-block partials in pss[], the
+    // last block to take a ticket sums them in block order.
+    float *pss;
+    uint32_t *ticket;
+    float *scale_out;
+    float norm_eps;
 };
 
 // Rows computed by one wave of the GEMV kernels.
@@ -58,7 +69,7 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n
                           hipStream_t s);
 hipError_t launch_embed(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
                         const StepState *st, const uint32_t *token_override, float embd_scale, float *x,
-                        hipStream_t s);
+                        float *scale_out, float norm_eps, hipStream_t s);
 hipError_t launch_get_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t row, float *out,
                           hipStream_t s);
 hipError_t launch_dequant(const uint8_t *blocks, uint32_t type, uint64_t n_blocks, float *out,

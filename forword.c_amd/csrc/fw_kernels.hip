@@ -22,15 +22,82 @@ namespace fw {
 
 // ── GEMV ─────────────────────────────────────────────────────────────────────
 
+// Deterministic block sum (butterfly within waves, waves in order); result in thread 0.
+__device__ __forceinline__ float block_sum_t0(float v, float *s_w)
+{
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) s_w[wave] = v;
+    __syncthreads();
+    float r = 0.f;
+    if (threadIdx.x == 0)
+        for (int w = 0; w < nw; w++) r += s_w[w];
+    return r;
+}
+
+// Last-block ticket: every block publishes its partial sum of squares; the last
+// block to arrive sums all partials in block order and publishes the RMSNorm
+// scale 1.0f/sqrtf(ss/n + eps) (norm.c:8-9).  No agent-scope fences.
+__device__ void publish_norm_scale(float part, float *pss, uint32_t *ticket, float *scale_out, uint32_t n,
+                                   float eps)
+{
+    __shared__ float s_w[16];
+    __shared__ bool s_last;
+    float b = block_sum_t0(part, s_w);
+    if (threadIdx.x == 0) {
+        st_sys(pss + blockIdx.x, b);
+        wait_mem();
+        s_last = ticket_sys(ticket) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    float v = 0.f;
+    for (uint32_t i = threadIdx.x; i < gridDim.x; i += blockDim.x) v += ld_sys(pss + i);
+    float ss = block_sum_t0(v, s_w);
+    if (threadIdx.x == 0) {
+        st_sys(scale_out, 1.0f / sqrtf((ss / (float)n) + eps));
+        st_sys(ticket, 0u);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void load_x(const float *xp, float *xv, bool vec4)
+{
+    if (vec4) {
+#pragma unroll
+        for (int i = 0; i < N / 4; i++) {
+            float4 v = reinterpret_cast<const float4 *>(xp)[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; i++) xv[i] = xp[i];
+    }
+}
+
+// x (and the norm weights when the input RMSNorm is folded in) for N columns at c0.
+template <int N>
+__device__ __forceinline__ void load_input(const QmvArgs &a, size_t c0, float *xv, bool vec4, float scale)
+{
+    load_x<N>(a.x + c0, xv, vec4);
+    if (a.norm_w) {
+        float wv[N];
+        load_x<N>(a.norm_w + c0, wv, vec4 && ((uintptr_t)a.norm_w & 15) == 0);
+#pragma unroll
+        for (int i = 0; i < N; i++) xv[i] = (xv[i] * wv[i]) * scale;     // simd_mul then simd_scale
+    }
+}
+
 template <uint32_t T, int EPI, bool PAIR>
 __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
 {
     constexpr int R = kRowsPerWave;
     const int lane = threadIdx.x & 63;
     const uint32_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (g >= a.n_groups) return;
-    if (EPI == EPI_STORE && a.state && a.state->greedy && a.state->pos + 1 < a.state->n_prompt)
-        return;   // greedy prefill: these logits are never read
+    const bool active = g < a.n_groups &&
+        !(EPI == EPI_STORE && a.state && a.state->greedy && a.state->pos + 1 < a.state->n_prompt);
+    // (greedy prefill: the logits of prompt positions before the last are never read)
 
     int seg = 0;
     if (EPI != EPI_SWIGLU)
@@ -43,7 +110,7 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
         int s = seg;
         if (EPI == EPI_SWIGLU) { s = k < R / 2 ? 0 : 1; row[k] = g * (R / 2) + (k % (R / 2)); }
         else row[k] = (g - a.group_base[seg]) * R + k;
-        ok[k] = row[k] < a.rows[s];
+        ok[k] = active && row[k] < a.rows[s];
         wr[k] = a.w[s] + (size_t)(ok[k] ? row[k] : 0) * a.row_bytes;
     }
 
@@ -51,10 +118,14 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
 #pragma unroll
     for (int k = 0; k < R; k++) acc[k] = 0.0f;
     const bool xv4 = ((uintptr_t)a.x & 15) == 0;
+    const float nscale = (active && a.norm_w) ? ld_sys(a.norm_scale) : 1.0f;
 
-    if constexpr (T == kF32) {
+    if (!active) {
+        // idle wave: only takes part in the block-wide epilogue below
+    } else if constexpr (T == kF32) {
         for (uint32_t c = lane; c < a.n_cols; c += 64) {
-            float xc = a.x[c];
+            float xc;
+            load_input<1>(a, c, &xc, false, nscale);
 #pragma unroll
             for (int k = 0; k < R; k++)
                 if (ok[k]) acc[k] = __builtin_fmaf(reinterpret_cast<const float *>(wr[k])[c], xc, acc[k]);
@@ -63,18 +134,12 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
         constexpr int BB = Blk<T>::bytes, NDW = Blk<T>::pair_dw;
         const uint32_t n_pairs = a.n_cols / 64;
         for (uint32_t p = lane; p < n_pairs; p += 64) {
+            uint32_t dw[R][NDW];
+#pragma unroll
+            for (int k = 0; k < R; k++)
+                if (ok[k]) load_pair<T>(wr[k] + (size_t)p * (2 * BB), dw[k]);
             float xv[64];
-            const float *xp = a.x + 64 * (size_t)p;
-            if (xv4) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    float4 v = reinterpret_cast<const float4 *>(xp)[i];
-                    xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 64; i++) xv[i] = xp[i];
-            }
+            load_input<64>(a, 64 * (size_t)p, xv, xv4, nscale);
             float sx0 = 0.f, sx1 = 0.f;
             if constexpr (T != kQ8_0) {
                 float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -83,10 +148,6 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
                 sx0 = s0 + s1;
                 sx1 = s2 + s3;
             }
-            uint32_t dw[R][NDW];
-#pragma unroll
-            for (int k = 0; k < R; k++)
-                if (ok[k]) load_pair<T>(wr[k] + (size_t)p * (2 * BB), dw[k]);
 #pragma unroll
             for (int k = 0; k < R; k++)
                 if (ok[k]) acc[k] += dot_pair<T>(dw[k], xv, sx0, sx1);
@@ -96,17 +157,7 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
         const uint32_t n_blocks = a.n_cols / 32;
         for (uint32_t b = lane; b < n_blocks; b += 64) {
             float xv[32];
-            const float *xp = a.x + 32 * (size_t)b;
-            if (xv4) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    float4 v = reinterpret_cast<const float4 *>(xp)[i];
-                    xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 32; i++) xv[i] = xp[i];
-            }
+            load_input<32>(a, 32 * (size_t)b, xv, xv4, nscale);
             float sx = 0.f;
             if constexpr (T != kQ8_0) {
                 float s0 = 0.f, s1 = 0.f;
@@ -122,44 +173,51 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
 
 #pragma unroll
     for (int k = 0; k < R; k++) acc[k] = wave_sum(acc[k]);
-    if (lane != 0) return;
 
     if constexpr (EPI == EPI_STORE) {
+        if (lane == 0)
 #pragma unroll
-        for (int k = 0; k < R; k++)
-            if (ok[k]) a.out[seg][row[k]] = acc[k];
+            for (int k = 0; k < R; k++)
+                if (ok[k]) a.out[seg][row[k]] = acc[k];
     } else if constexpr (EPI == EPI_RESID) {
+        float ss = 0.f;
+        if (lane == 0)
 #pragma unroll
-        for (int k = 0; k < R; k++)
-            if (ok[k]) {
-                float v = a.out[0][row[k]] + acc[k];          // x[i] += y[i] (transformer.c:271-272)
-                a.out[0][row[k]] = v;
-                if (a.trace) a.trace[row[k]] = v;
-            }
+            for (int k = 0; k < R; k++)
+                if (ok[k]) {
+                    float v = a.out[0][row[k]] + acc[k];          // x[i] += y[i] (transformer.c:271-272)
+                    a.out[0][row[k]] = v;
+                    if (a.trace) a.trace[row[k]] = v;
+                    ss = __builtin_fmaf(v, v, ss);
+                }
+        if (a.scale_out) publish_norm_scale(ss, a.pss, a.ticket, a.scale_out, a.rows[0], a.norm_eps);
     } else if constexpr (EPI == EPI_SWIGLU) {
+        if (lane == 0)
 #pragma unroll
-        for (int k = 0; k < R / 2; k++)
-            if (ok[k]) a.out[0][row[k]] = silu_ref(acc[k]) * acc[k + R / 2];   // ffn.c:88-104
+            for (int k = 0; k < R / 2; k++)
+                if (ok[k]) a.out[0][row[k]] = silu_ref(acc[k]) * acc[k + R / 2];   // ffn.c:88-104
     } else {   // EPI_QKV: RoPE on q and k rows (rope.c:37-43), then q out / KV append at pos
-        const uint32_t pos = a.state->pos, half = a.head_dim / 2;
-        const uint32_t role = seg + a.role_base;
-        float v[R];
+        if (lane == 0 && active) {
+            const uint32_t pos = a.state->pos, half = a.head_dim / 2;
+            const uint32_t role = seg + a.role_base;
+            float v[R];
 #pragma unroll
-        for (int k = 0; k < R; k++) v[k] = acc[k];
-        if (role < 2) {
+            for (int k = 0; k < R; k++) v[k] = acc[k];
+            if (role < 2) {
 #pragma unroll
-            for (int k = 0; k < R; k += 2) {
-                uint32_t i = (row[k] % a.head_dim) / 2;
-                float c = a.cos_tab[(size_t)pos * half + i], s = a.sin_tab[(size_t)pos * half + i];
-                float v0 = v[k], v1 = v[k + 1];
-                v[k] = v0 * c - v1 * s;
-                v[k + 1] = v0 * s + v1 * c;
+                for (int k = 0; k < R; k += 2) {
+                    uint32_t i = (row[k] % a.head_dim) / 2;
+                    float c = a.cos_tab[(size_t)pos * half + i], s = a.sin_tab[(size_t)pos * half + i];
+                    float v0 = v[k], v1 = v[k + 1];
+                    v[k] = v0 * c - v1 * s;
+                    v[k + 1] = v0 * s + v1 * c;
+                }
             }
-        }
-        float *dst = role == 0 ? a.out[0] : a.out[role] + (size_t)pos * a.kv_dim;
+            float *dst = role == 0 ? a.out[0] : a.out[role] + (size_t)pos * a.kv_dim;
 #pragma unroll
-        for (int k = 0; k < R; k++)
-            if (ok[k]) dst[row[k]] = v[k];
+            for (int k = 0; k < R; k++)
+                if (ok[k]) dst[row[k]] = v[k];
+        }
     }
 }
 
@@ -230,17 +288,33 @@ hipError_t launch_qmv(uint32_t type, int epi, QmvArgs a, hipStream_t s)
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w,
                                                   float *__restrict__ out, uint32_t n, float eps)
 {
+    extern __shared__ float s_x[];                 // x staged once (n <= 16384), else read from global
     __shared__ float s_scale;
+    const bool staged = n <= 16384;
+    if (staged) {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) s_x[i] = x[i];
+        __syncthreads();
+    }
+    const float *xs = staged ? s_x : x;
     if (threadIdx.x < 64) {
         const int L = threadIdx.x;
         const uint32_t n16 = n / 16 * 16;
         float acc = 0.0f;
-        if (L < 16)
-            for (uint32_t i = L; i < n16; i += 16) acc = __builtin_fmaf(x[i], x[i], acc);
+        if (L < 16) {
+            uint32_t i = L;
+            for (; i + 48 < n16; i += 64) {        // 4 loads in flight per step, same FMA order
+                float a0 = xs[i], a1 = xs[i + 16], a2 = xs[i + 32], a3 = xs[i + 48];
+                acc = __builtin_fmaf(a0, a0, acc);
+                acc = __builtin_fmaf(a1, a1, acc);
+                acc = __builtin_fmaf(a2, a2, acc);
+                acc = __builtin_fmaf(a3, a3, acc);
+            }
+            for (; i < n16; i += 16) acc = __builtin_fmaf(xs[i], xs[i], acc);
+        }
         float hi = __shfl_down(acc, 8, 64);
         if (L < 8) {
             acc = acc + hi;
-            if (n16 + 8 <= n) acc = __builtin_fmaf(x[n16 + L], x[n16 + L], acc);
+            if (n16 + 8 <= n) acc = __builtin_fmaf(xs[n16 + L], xs[n16 + L], acc);
         }
         float a4 = __shfl_down(acc, 4, 64);
         float s = acc + a4;                       // lanes 0..3: lo128 + hi128
@@ -249,7 +323,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
         float t1 = __shfl_down(t, 1, 64);
         if (L == 0) {
             float sum = 0.0f + (t + t1);
-            for (uint32_t i = n / 8 * 8; i < n; i++) sum = sum + x[i] * x[i];
+            for (uint32_t i = n / 8 * 8; i < n; i++) sum = sum + xs[i] * xs[i];
             s_scale = 1.0f / sqrtf((sum / (float)n) + eps);
         }
     }
@@ -263,7 +337,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n, float eps, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, s, x, w, out, n, eps);
+    size_t lds = n <= 16384 ? (size_t)n * 4 : 0;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), lds, s, x, w, out, n, eps);
     return hipGetLastError();
 }
 
@@ -290,12 +365,14 @@ __device__ __forceinline__ uint32_t block_bytes_dev(uint32_t t)
     return t == kQ4_0 ? 18u : t == kQ5_0 ? 22u : 34u;
 }
 
-__global__ void k_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
-                      const StepState *st, const uint32_t *tok_override, uint32_t row_fixed,
-                      float embd_scale, float *out)
+__global__ __launch_bounds__(1024) void k_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
+                                              const StepState *st, const uint32_t *tok_override, uint32_t row_fixed,
+                                              float embd_scale, float *out, float *scale_out, float eps)
 {
+    __shared__ float s_w[16];
     uint32_t row = st ? st->token : (tok_override ? *tok_override : row_fixed);
     if (row >= n_rows) row = n_rows - 1;            // bounds were checked on the host
+    float ss = 0.f;
     for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n_cols; j += gridDim.x * blockDim.x) {
         float v;
         if (type == kF32) v = reinterpret_cast<const float *>(w)[(size_t)row * n_cols + j];
@@ -304,18 +381,22 @@ __global__ void k_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t
             const uint8_t *blk = w + (size_t)row * (n_cols / 32) * bb + (size_t)(j / 32) * bb;
             v = dequant_one(blk, type, j & 31);
         }
-        if (embd_scale != 1.0f) v *= embd_scale;
+        if (embd_scale != 1.0f) v *= embd_scale;               // transformer.c:179-182
         out[j] = v;
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    if (scale_out) {                                            // launched as one block
+        float t = block_sum_t0(ss, s_w);
+        if (threadIdx.x == 0) st_sys(scale_out, 1.0f / sqrtf((t / (float)n_cols) + eps));
     }
 }
 
 hipError_t launch_embed(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
                         const StepState *st, const uint32_t *token_override, float embd_scale, float *x,
-                        hipStream_t s)
+                        float *scale_out, float norm_eps, hipStream_t s)
 {
-    uint32_t blocks = (n_cols + 255) / 256;
-    hipLaunchKernelGGL(k_row, dim3(blocks), dim3(256), 0, s, w, type, n_cols, n_rows, st, token_override,
-                       0u, embd_scale, x);
+    hipLaunchKernelGGL(k_row, dim3(1), dim3(1024), 0, s, w, type, n_cols, n_rows, st, token_override, 0u,
+                       embd_scale, x, scale_out, norm_eps);
     return hipGetLastError();
 }
 
@@ -324,7 +405,7 @@ hipError_t launch_get_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint
 {
     uint32_t blocks = (n_cols + 255) / 256;
     hipLaunchKernelGGL(k_row, dim3(blocks), dim3(256), 0, s, w, type, n_cols, row + 1u,
-                       (const StepState *)nullptr, (const uint32_t *)nullptr, row, 1.0f, out);
+                       (const StepState *)nullptr, (const uint32_t *)nullptr, row, 1.0f, out, (float *)nullptr, 0.f);
     return hipGetLastError();
 }
 
@@ -441,25 +522,29 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ q, const
     }
 }
 
-__global__ void k_attn_combine(const float *__restrict__ part, float *__restrict__ out, uint32_t n_splits,
-                               uint32_t hd)
+__global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part, float *__restrict__ out,
+                                                       uint32_t n_splits, uint32_t hd)
 {
-    const uint32_t h = blockIdx.x;
+    __shared__ float s_wt[256], s_red[8];
+    const uint32_t h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float *base = part + (size_t)h * n_splits * (hd + 2);
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < n_splits; s++) M = fmaxf(M, base[(size_t)s * (hd + 2) + hd]);
-    float L = 0.f;
-    for (uint32_t s = 0; s < n_splits; s++) {
-        float ms = base[(size_t)s * (hd + 2) + hd];
-        if (ms != -INFINITY) L = __builtin_fmaf(base[(size_t)s * (hd + 2) + hd + 1], exp2f(ms - M), L);
-    }
-    const float inv = 1.0f / L;
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    // one split per thread (n_splits <= 256): its max and weight
+    float ms = t < n_splits ? base[(size_t)t * (hd + 2) + hd] : -INFINITY;
+    float M = wave_max(ms);
+    if (lane == 0) s_red[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float wt = (t < n_splits && ms != -INFINITY) ? exp2f(ms - M) : 0.f;
+    s_wt[t] = wt;
+    float lw = t < n_splits ? base[(size_t)t * (hd + 2) + hd + 1] * wt : 0.f;
+    lw = wave_sum(lw);
+    __syncthreads();
+    if (lane == 0) s_red[4 + wave] = lw;
+    __syncthreads();
+    const float inv = 1.0f / ((s_red[4] + s_red[5]) + (s_red[6] + s_red[7]));
+    for (uint32_t d = t; d < hd; d += blockDim.x) {
         float O = 0.f;
-        for (uint32_t s = 0; s < n_splits; s++) {
-            float ms = base[(size_t)s * (hd + 2) + hd];
-            if (ms != -INFINITY) O = __builtin_fmaf(base[(size_t)s * (hd + 2) + d], exp2f(ms - M), O);
-        }
+        for (uint32_t s = 0; s < n_splits; s++) O = __builtin_fmaf(base[(size_t)s * (hd + 2) + d], s_wt[s], O);
         out[(size_t)h * hd + d] = O * inv;
     }
 }
@@ -512,7 +597,7 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc, fl
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(hd < 128 ? 64 : 128), 0, s, part, out, n_splits, hd);
+    hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(256), 0, s, part, out, n_splits, hd);
     return hipGetLastError();
 }
 
@@ -573,26 +658,26 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, uin
     }
     block_argmax(bv, bi);
     if (threadIdx.x == 0) {
-        pv[blockIdx.x] = bv;
-        pi[blockIdx.x] = bi;
-        __threadfence();
-        s_last = atomicAdd(counter, 1u) == gridDim.x - 1;
+        st_sys(pv + blockIdx.x, bv);
+        st_sys(pi + blockIdx.x, bi);
+        wait_mem();
+        s_last = ticket_sys(counter) == gridDim.x - 1;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     bv = -INFINITY;
     bi = 0xffffffffu;
     for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
-        float v = __builtin_nontemporal_load(pv + b);
-        uint32_t i = __builtin_nontemporal_load(pi + b);
+        float v = ld_sys(pv + b);
+        uint32_t i = ld_sys(pi + b);
         if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
     }
+    __syncthreads();
     block_argmax(bv, bi);
     if (threadIdx.x == 0) {
         uint32_t r = (bi == 0xffffffffu || isnan(x[0])) ? 0u : bi;
         *out = r;
-        *counter = 0u;
+        st_sys(counter, 0u);
         if (st) {
             st->next = r;
             if (st->greedy) greedy_advance(st, prompt, ids, r);

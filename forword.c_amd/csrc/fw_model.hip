@@ -83,6 +83,8 @@ struct forword_gpu {
     float *d_x = nullptr, *d_xn = nullptr, *d_q = nullptr, *d_att = nullptr, *d_h = nullptr;
     float *d_logits = nullptr, *d_part = nullptr, *d_trace = nullptr, *d_pv = nullptr;
     uint32_t *d_pi = nullptr, *d_counter = nullptr, *d_argmax = nullptr, *d_prompt = nullptr, *d_ids = nullptr;
+    float *d_pss = nullptr, *d_scale = nullptr;      // RMSNorm scale published by the residual kernels
+    uint32_t *d_ticket = nullptr;
     StepState *d_state = nullptr, *h_state = nullptr;
     float *h_logits = nullptr;
     uint32_t *h_u32 = nullptr;
@@ -167,11 +169,14 @@ static hipError_t enqueue_step(forword_gpu_t *h)
     hipStream_t s = h->stream;
     hipError_t e;
 #define TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
-    TRY(launch_embed(h->embd.w, h->embd.type, n, h->embd.out, h->d_state, nullptr, c.embd_scale, h->d_x, s));
+    // Every RMSNorm (transformer.c:261,279,293-304) is folded into the GEMV that
+    // consumes it: the kernel writing x (embedding, Wo and down residuals)
+    // publishes the scale, the next GEMV applies (x*w)*scale as it loads x.
+    TRY(launch_embed(h->embd.w, h->embd.type, n, h->embd.out, h->d_state, nullptr, c.embd_scale, h->d_x,
+                     h->d_scale, c.norm_eps, s));
     for (uint32_t l = 0; l < c.n_layer; l++) {
         const Layer &Ly = h->L[l];
         float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
-        TRY(launch_rmsnorm(h->d_x, Ly.attn_norm, h->d_xn, n, c.norm_eps, s));          // transformer.c:261
         // attention_forward (attention.c:124-140): Q/K/V, RoPE, KV append at pos
         const Lin *qkv[3] = { &Ly.q, &Ly.k, &Ly.v };
         const bool fused = Ly.q.type == Ly.k.type && Ly.k.type == Ly.v.type;
@@ -182,7 +187,8 @@ static hipError_t enqueue_step(forword_gpu_t *h)
             a.role_base = s0;
             a.n_cols = n;
             a.row_bytes = qkv[s0]->row_bytes;
-            a.x = h->d_xn;
+            a.x = h->d_x;
+            a.norm_w = Ly.attn_norm; a.norm_scale = h->d_scale;
             a.out[0] = h->d_q; a.out[1] = kc; a.out[2] = vc;
             a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
             a.state = h->d_state;
@@ -197,14 +203,15 @@ static hipError_t enqueue_step(forword_gpu_t *h)
             QmvArgs a{};                                                                // attention.c:166 + transformer.c:271
             a.n_seg = 1; a.w[0] = Ly.o.w; a.rows[0] = Ly.o.out; a.n_cols = Ly.o.in; a.row_bytes = Ly.o.row_bytes;
             a.x = h->d_att; a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l) * n;
+            a.pss = h->d_pss; a.ticket = h->d_ticket; a.scale_out = h->d_scale; a.norm_eps = c.norm_eps;
             qmv_plan(a, EPI_RESID);
             TRY(launch_qmv(Ly.o.type, EPI_RESID, a, s));
         }
-        TRY(launch_rmsnorm(h->d_x, Ly.ffn_norm, h->d_xn, n, c.norm_eps, s));           // transformer.c:279
         {
             QmvArgs a{};                                                                // ffn.c:82-104
             a.n_seg = 2; a.w[0] = Ly.gate.w; a.w[1] = Ly.up.w; a.rows[0] = a.rows[1] = c.n_ff;
-            a.n_cols = n; a.row_bytes = Ly.gate.row_bytes; a.x = h->d_xn; a.out[0] = h->d_h;
+            a.n_cols = n; a.row_bytes = Ly.gate.row_bytes; a.x = h->d_x; a.out[0] = h->d_h;
+            a.norm_w = Ly.ffn_norm; a.norm_scale = h->d_scale;
             qmv_plan(a, EPI_SWIGLU);
             TRY(launch_qmv(Ly.gate.type, EPI_SWIGLU, a, s));
         }
@@ -212,16 +219,16 @@ static hipError_t enqueue_step(forword_gpu_t *h)
             QmvArgs a{};                                                                // ffn.c:106 + transformer.c:287
             a.n_seg = 1; a.w[0] = Ly.down.w; a.rows[0] = n; a.n_cols = c.n_ff; a.row_bytes = Ly.down.row_bytes;
             a.x = h->d_h; a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l + 1) * n;
+            a.pss = h->d_pss; a.ticket = h->d_ticket; a.scale_out = h->d_scale; a.norm_eps = c.norm_eps;
             qmv_plan(a, EPI_RESID);
             TRY(launch_qmv(Ly.down.type, EPI_RESID, a, s));
         }
     }
-    if (h->out_norm) TRY(launch_rmsnorm(h->d_x, h->out_norm, h->d_xn, n, c.norm_eps, s));  // transformer.c:293-304
-    else TRY(hipMemcpyAsync(h->d_xn, h->d_x, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
     {
-        QmvArgs a{};                                                                    // transformer.c:310-323
+        QmvArgs a{};                                                                    // transformer.c:293-323
         a.n_seg = 1; a.w[0] = h->out.w; a.rows[0] = h->out.out; a.n_cols = n; a.row_bytes = h->out.row_bytes;
-        a.x = h->d_xn; a.out[0] = h->d_logits; a.state = h->d_state;
+        a.x = h->d_x; a.out[0] = h->d_logits; a.state = h->d_state;
+        a.norm_w = h->out_norm; a.norm_scale = h->d_scale;       // no output_norm: logits of x itself
         qmv_plan(a, EPI_STORE);
         TRY(launch_qmv(h->out.type, EPI_STORE, a, s));
     }
@@ -374,7 +381,9 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         dalloc(h, (void **)&h->d_pv, h->am_blocks * 4, "argmax") || dalloc(h, (void **)&h->d_pi, h->am_blocks * 4, "argmax") ||
         dalloc(h, (void **)&h->d_counter, 4, "argmax") || dalloc(h, (void **)&h->d_argmax, 4, "argmax") ||
         dalloc(h, (void **)&h->d_prompt, max_ctx * 4, "prompt") || dalloc(h, (void **)&h->d_ids, (max_ctx + 1) * 4, "ids") ||
-        dalloc(h, (void **)&h->d_state, sizeof(StepState), "state"))
+        dalloc(h, (void **)&h->d_state, sizeof(StepState), "state") ||
+        dalloc(h, (void **)&h->d_pss, ((size_t)n / 16 + 64) * 4, "norm partials") ||
+        dalloc(h, (void **)&h->d_scale, 64, "norm scale") || dalloc(h, (void **)&h->d_ticket, 64, "norm ticket"))
         FAIL();
     if (hipHostMalloc((void **)&h->h_state, sizeof(StepState), 0) != hipSuccess ||
         hipHostMalloc((void **)&h->h_logits, (size_t)c.n_vocab * 4, 0) != hipSuccess ||
@@ -385,6 +394,7 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
     memset(h->h_state, 0, sizeof(StepState));
     if (hipMemset(h->d_k, 0, kv_elems * 4) != hipSuccess || hipMemset(h->d_v, 0, kv_elems * 4) != hipSuccess ||
         hipMemset(h->d_counter, 0, 4) != hipSuccess || hipMemset(h->d_state, 0, sizeof(StepState)) != hipSuccess ||
+        hipMemset(h->d_ticket, 0, 64) != hipSuccess || hipMemset(h->d_scale, 0, 64) != hipSuccess ||
         hipMemset(h->d_trace, 0, (size_t)2 * c.n_layer * n * 4) != hipSuccess ||
         hipMemcpy(h->d_cos, cos_tab, max_ctx * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(h->d_sin, sin_tab, max_ctx * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
