@@ -162,7 +162,8 @@ def main():
     hip = Hip()
     t0 = time.perf_counter()
     gm = fwgpu.GpuModel(host)
-    log(f"uploaded to HBM in {time.perf_counter() - t0:.1f}s")
+    step_impl = "persistent kernel" if gm.persistent else "per-phase kernels (hipGraph)"
+    log(f"uploaded to HBM in {time.perf_counter() - t0:.1f}s; token step: {step_impl}")
     stream = gm.stream
     prompt = np.random.default_rng(512).integers(3, host.cfg.n_vocab, args.prompt).astype(np.uint32)
 
@@ -183,6 +184,12 @@ def main():
     avg_bytes = float(np.mean([step_bytes(host.cfg, p) for p in range(p0, p0 + args.steps)]))
     log(f"decode: {args.steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s, "
         f"{avg_bytes * tok_s / 1e9:.0f} GB/s effective")
+    if gm.persistent and os.environ.get("FORWORD_GPU_PHASE_TIMES") == "1":
+        pt, L = gm.phase_times(), host.cfg.n_layer
+        names = ["qkv", "attn", "wo", "ffn", "down"]
+        per = {nm: float(np.mean(pt[i:5 * L:5])) for i, nm in enumerate(names)}
+        log("phase us (mean over layers, last launch): " + ", ".join(f"{k} {v:.2f}" for k, v in per.items())
+            + f", head {pt[-1]:.2f}; step {pt.sum():.1f}")
 
     algo, dur_ms, dur_ms_total, copies = time_dominant_kernel(hip, stream, host.cfg.n_embd, host.cfg.n_ff)
     achieved = algo / (dur_ms / 1e3) / 1e9
@@ -202,7 +209,7 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded random-init GGUF, random prompt ids)",
-        "config": {"workload": workload, "prompt_tokens": args.prompt,
+        "config": {"workload": workload, "prompt_tokens": args.prompt, "step_impl": step_impl,
                    "decode_positions": [p0, p0 + args.steps - 1], "kv_cache": "fp32 in HBM",
                    "step_bytes_avg": int(avg_bytes), "step_gbs": round(avg_bytes * tok_s / 1e9, 1),
                    "step_roofline_frac": round(avg_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),

@@ -22,6 +22,17 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 typedef u32x2 u32x2_a4 __attribute__((aligned(4)));
 
+// Global-memory (address space 1) views of generic pointers.  Pointers that
+// the kernels read out of memory (phase descriptors) are generic to the
+// compiler, which then emits flat loads; those also count on lgkmcnt, so every
+// LDS access would wait for all outstanding weight loads.
+#define FW_GLOBAL __attribute__((address_space(1)))
+template <typename T> __device__ __forceinline__ const FW_GLOBAL T *gptr(const T *p)
+{
+    return (const FW_GLOBAL T *)p;
+}
+template <typename T> __device__ __forceinline__ FW_GLOBAL T *gptr(T *p) { return (FW_GLOBAL T *)p; }
+
 template <uint32_t T> struct Blk;
 template <> struct Blk<kQ4_0> { static constexpr int bytes = 18, pair_dw = 9; };
 template <> struct Blk<kQ5_0> { static constexpr int bytes = 22, pair_dw = 11; };
@@ -139,24 +150,24 @@ __device__ __forceinline__ float dot_pair(const uint32_t *dw, const float *x, fl
 template <uint32_t T>
 __device__ __forceinline__ void load_pair(const uint8_t *p, uint32_t *dw)
 {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(p);
+    const FW_GLOBAL uint32_t *w = gptr(reinterpret_cast<const uint32_t *>(p));
     if constexpr (T == kQ4_0) {                       // 36 B = 16 + 16 + 4
-        u32x4 a = *reinterpret_cast<const u32x4_a4 *>(w);
-        u32x4 b = *reinterpret_cast<const u32x4_a4 *>(w + 4);
+        u32x4 a = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(w);
+        u32x4 b = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(w + 4);
         dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
         dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
         dw[8] = w[8];
     } else if constexpr (T == kQ5_0) {                // 44 B = 16 + 16 + 8 + 4
-        u32x4 a = *reinterpret_cast<const u32x4_a4 *>(w);
-        u32x4 b = *reinterpret_cast<const u32x4_a4 *>(w + 4);
-        u32x2 c = *reinterpret_cast<const u32x2_a4 *>(w + 8);
+        u32x4 a = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(w);
+        u32x4 b = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(w + 4);
+        u32x2 c = *reinterpret_cast<const FW_GLOBAL u32x2_a4 *>(w + 8);
         dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
         dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
         dw[8] = c.x; dw[9] = c.y; dw[10] = w[10];
     } else {                                          // 68 B = 4*16 + 4
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            u32x4 a = *reinterpret_cast<const u32x4_a4 *>(w + 4 * k);
+            u32x4 a = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(w + 4 * k);
             dw[4 * k] = a.x; dw[4 * k + 1] = a.y; dw[4 * k + 2] = a.z; dw[4 * k + 3] = a.w;
         }
         dw[16] = w[16];
@@ -188,6 +199,28 @@ __device__ __forceinline__ float dot_single(const uint8_t *p, const float *x, fl
     }
 }
 
+// Element j (0..31) of one block, exactly as the reference dequantises it.
+__device__ __forceinline__ float dequant_one(const uint8_t *blk, uint32_t type, uint32_t j)
+{
+    float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    if (type == kQ8_0) return d * (float)(int8_t)blk[2 + j];                    // quant.c:258
+    if (type == kQ4_0) {
+        uint32_t b = blk[2 + (j & 15)];
+        int q = (int)(j < 16 ? (b & 15u) : (b >> 4));
+        return d * (float)(q - 8);
+    }
+    uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                  ((uint32_t)blk[5] << 24);
+    uint32_t b = blk[6 + (j & 15)];
+    int q = (int)((j < 16 ? (b & 15u) : (b >> 4)) | (((qh >> j) & 1u) << 4));
+    return d * (float)(q - 16);                                                 // quant_matvec.c:204-212
+}
+
+__device__ __forceinline__ uint32_t block_bytes_dev(uint32_t t)
+{
+    return t == kQ4_0 ? 18u : t == kQ5_0 ? 22u : 34u;
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v)
 {
@@ -211,23 +244,34 @@ __device__ __forceinline__ float wave_max(float v)
 // explicit wait for this wave's outstanding memory operations.
 __device__ __forceinline__ void st_sys(float *p, float v)
 {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ void st_sys(uint32_t *p, uint32_t v)
 {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ float ld_sys(const float *p)
 {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load(gptr(const_cast<float *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ uint32_t ld_sys(const uint32_t *p)
 {
-    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load(gptr(const_cast<uint32_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// Two floats at an 8-byte aligned address.  Atomic loads are not reordered by
+// the compiler, so callers issue a batch of them before using any result.
+__device__ __forceinline__ float2v ld_sys2(const float *p)
+{
+    const uint64_t v = __hip_atomic_load(gptr(reinterpret_cast<uint64_t *>(const_cast<float *>(p))), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_SYSTEM);
+    float2v r;
+    r[0] = __builtin_bit_cast(float, (uint32_t)v);
+    r[1] = __builtin_bit_cast(float, (uint32_t)(v >> 32));
+    return r;
 }
 __device__ __forceinline__ uint32_t ticket_sys(uint32_t *p)
 {
-    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_fetch_add(gptr(p), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 // s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0): every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }

@@ -344,27 +344,6 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n
 
 // ── dequantisation: embedding row, get_row, bulk ─────────────────────────────
 
-__device__ __forceinline__ float dequant_one(const uint8_t *blk, uint32_t type, uint32_t j)
-{
-    float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    if (type == kQ8_0) return d * (float)(int8_t)blk[2 + j];                    // quant.c:258
-    if (type == kQ4_0) {
-        uint32_t b = blk[2 + (j & 15)];
-        int q = (int)(j < 16 ? (b & 15u) : (b >> 4));
-        return d * (float)(q - 8);
-    }
-    uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
-                  ((uint32_t)blk[5] << 24);
-    uint32_t b = blk[6 + (j & 15)];
-    int q = (int)((j < 16 ? (b & 15u) : (b >> 4)) | (((qh >> j) & 1u) << 4));
-    return d * (float)(q - 16);                                                 // quant_matvec.c:204-212
-}
-
-__device__ __forceinline__ uint32_t block_bytes_dev(uint32_t t)
-{
-    return t == kQ4_0 ? 18u : t == kQ5_0 ? 22u : 34u;
-}
-
 __global__ __launch_bounds__(1024) void k_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
                                               const StepState *st, const uint32_t *tok_override, uint32_t row_fixed,
                                               float embd_scale, float *out, float *scale_out, float eps)

@@ -5,10 +5,16 @@
 // RoPE + KV append, split-K attention, Wo GEMV + residual, RMSNorm, fused
 // gate/up GEMV + SiLU*up, down GEMV + residual] -> RMSNorm -> lm-head GEMV ->
 // argmax.  The step reads token and position from a small device-resident
-// StepState, so it is captured once as a hipGraph and replayed for every
-// position; the greedy loop (main.c:145-217) replays it back to back with the
-// argmax kernel feeding the next token on the device.
+// StepState, so the greedy loop (main.c:145-217) runs on the device: the
+// argmax feeds the next token without a host round trip.
+//
+// Two implementations of the step: for models whose layer linears share one
+// Q4_0/Q5_0/Q8_0 type, a persistent cooperative kernel runs whole steps (up to
+// 64 per launch) with grid barriers between phases (fw_step.hip); otherwise
+// (or with FORWORD_GPU_MEGAKERNEL=0) one kernel per phase, captured once as a
+// hipGraph and replayed per position.
 #include "fw_kernels.h"
+#include "fw_step.h"
 #include "forword_gpu.h"
 
 #include <hip/hip_runtime.h>
@@ -92,6 +98,16 @@ struct forword_gpu {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool traced = false;
+    // persistent step kernel
+    bool mk = false;
+    uint32_t mk_wg = 0, mk_tl = 0, mk_th = 0, mk_epoch = 0;
+    size_t mk_lds = 0;
+    MkArgs mka{};
+    uint32_t *d_bar = nullptr, *d_mk_err = nullptr, *d_mk_tickets = nullptr, *d_ami = nullptr;
+    float *d_amv = nullptr, *d_mk_part = nullptr;
+    MkOp *d_ops = nullptr;
+    uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
+    uint32_t prof_steps = 0;
     std::vector<void *> allocs;
 };
 
@@ -238,10 +254,147 @@ static hipError_t enqueue_step(forword_gpu_t *h)
     return hipSuccess;
 }
 
-static int run_step(forword_gpu_t *h)
+static constexpr uint32_t kMkStepsPerLaunch = 64;
+
+// Queue n token steps.
+static int run_steps(forword_gpu_t *h, size_t n)
 {
-    if (h->exec) HIPCHK(hipGraphLaunch(h->exec, h->stream), "hipGraphLaunch");
-    else HIPCHK(enqueue_step(h), "token step launch");
+    if (h->mk) {
+        while (n) {
+            const uint32_t k = n > kMkStepsPerLaunch ? kMkStepsPerLaunch : (uint32_t)n;
+            MkArgs a = h->mka;
+            a.epoch0 = h->mk_epoch;
+            a.n_steps = k;
+            HIPCHK(mk_launch(a, h->mk_tl, h->mk_th, h->mk_wg, h->mk_lds, h->stream), "persistent step launch");
+            h->prof_steps = k;
+            h->mk_epoch += k * mk_barriers_per_step(h->cfg.n_layer);
+            n -= k;
+        }
+        return 0;
+    }
+    for (size_t i = 0; i < n; i++) {
+        if (h->exec) HIPCHK(hipGraphLaunch(h->exec, h->stream), "hipGraphLaunch");
+        else HIPCHK(enqueue_step(h), "token step launch");
+    }
+    return 0;
+}
+
+// After the stream has drained: did a persistent launch give up at a barrier?
+// Then its results are invalid; reset the barrier state for the next launch.
+static int mk_check(forword_gpu_t *h)
+{
+    if (!h->mk) return 0;
+    uint32_t err = 0;
+    HIPCHK(hipMemcpy(&err, h->d_mk_err, 4, hipMemcpyDeviceToHost), "persistent step status");
+    if (!err) return 0;
+    (void)hipMemset(h->d_bar, 0, (size_t)h->mk_wg * 128);
+    (void)hipMemset(h->d_mk_tickets, 0, 64 * 4);
+    (void)hipMemset(h->d_mk_err, 0, 4);
+    (void)hipDeviceSynchronize();
+    h->mk_epoch = 0;
+    set_err("persistent step kernel: a grid barrier timed out; results of the last call are invalid");
+    return -1;
+}
+
+// Set up the persistent step kernel when the model and the device allow it
+// (else the per-phase kernels run).
+static int setup_mk(forword_gpu_t *h)
+{
+    const char *env = getenv("FORWORD_GPU_MEGAKERNEL");
+    if (env && !strcmp(env, "0")) return 0;
+    const forword_gpu_config_t &c = h->cfg;
+    const uint32_t n = c.n_embd, hd = c.head_dim, kvd = c.n_head_kv * hd, L = c.n_layer;
+    const uint32_t tl = h->L[0].q.type;
+    for (const Layer &Ly : h->L)
+        for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })
+            if (l->type != tl) return 0;
+    if (!mk_supported(n, c.n_ff, hd, c.n_head / c.n_head_kv, tl, h->out.type, h->embd.type) || c.n_head_kv + 1 > 64)
+        return 0;
+    int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 || cus > 512) {
+        (void)hipGetLastError();
+        return 0;
+    }
+
+    MkArgs &a = h->mka;
+    a.n_layer = L;
+    a.n_ops = 5 * L + 1;
+    a.embd = h->embd.w; a.embd_type = h->embd.type; a.embd_row_bytes = h->embd.row_bytes; a.embd_scale = c.embd_scale;
+    a.n_embd = n; a.n_ff = c.n_ff; a.n_head = c.n_head; a.n_kv = c.n_head_kv; a.head_dim = hd;
+    a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
+    a.kc = h->d_k; a.vc = h->d_v; a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
+    a.x = h->d_x; a.q = h->d_q; a.att = h->d_att; a.h = h->d_h; a.logits = h->d_logits;
+    a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
+    // (KV head, split) attention items: about one per workgroup, >= 8 positions per split
+    uint32_t ns = (uint32_t)cus / c.n_head_kv;
+    const uint32_t by_ctx = (uint32_t)((h->n_ctx + 7) / 8);
+    if (ns > by_ctx) ns = by_ctx;
+    if (ns > 256) ns = 256;
+    if (ns < 1) ns = 1;
+    a.n_splits = ns;
+    const size_t lds = mk_lds_bytes(a, (uint32_t)cus);
+    const int wg = mk_max_workgroups(tl, h->out.type, lds);
+    if (wg != cus) {
+        fprintf(stderr, "forword_gpu: persistent step kernel cannot launch (LDS %zu B); using per-phase kernels\n", lds);
+        return 0;
+    }
+
+    std::vector<MkOp> ops;
+    for (uint32_t l = 0; l < L; l++) {
+        const Layer &Ly = h->L[l];
+        MkOp q{}, at{}, o{}, f{}, d{};
+        q.kind = MK_QKV; q.layer = l; q.n_in = n; q.norm = Ly.attn_norm; q.src = h->d_x;
+        q.g.w[0] = Ly.q.w; q.g.w[1] = Ly.k.w; q.g.w[2] = Ly.v.w;
+        q.g.rows[0] = n; q.g.rows[1] = kvd; q.g.rows[2] = kvd; q.g.n_rows = n + 2 * kvd;
+        q.g.n_cols = n; q.g.row_bytes = Ly.q.row_bytes; q.g.type = tl;
+        at.kind = MK_ATTN; at.layer = l;
+        o.kind = MK_WO; o.layer = l; o.n_in = n; o.src = h->d_att; o.trace = h->d_trace + (size_t)(2 * l) * n;
+        o.g.w[0] = Ly.o.w; o.g.rows[0] = n; o.g.n_rows = n; o.g.n_cols = n; o.g.row_bytes = Ly.o.row_bytes; o.g.type = tl;
+        f.kind = MK_FFN; f.layer = l; f.n_in = n; f.norm = Ly.ffn_norm; f.src = h->d_x;
+        f.g.w[0] = Ly.gate.w; f.g.w[1] = Ly.up.w; f.g.rows[0] = f.g.rows[1] = c.n_ff; f.g.n_rows = c.n_ff;
+        f.g.n_cols = n; f.g.row_bytes = Ly.gate.row_bytes; f.g.type = tl;
+        d.kind = MK_DOWN; d.layer = l; d.n_in = c.n_ff; d.src = h->d_h; d.trace = h->d_trace + (size_t)(2 * l + 1) * n;
+        d.g.w[0] = Ly.down.w; d.g.rows[0] = n; d.g.n_rows = n; d.g.n_cols = c.n_ff; d.g.row_bytes = Ly.down.row_bytes;
+        d.g.type = tl;
+        for (const MkOp &op : { q, at, o, f, d }) ops.push_back(op);
+    }
+    MkOp head{};                                     // output_norm may be absent: logits of x itself
+    head.kind = MK_HEAD; head.layer = L; head.n_in = n; head.norm = h->out_norm; head.src = h->d_x;
+    head.g.w[0] = h->out.w; head.g.rows[0] = c.n_vocab; head.g.n_rows = c.n_vocab; head.g.n_cols = n;
+    head.g.row_bytes = h->out.row_bytes; head.g.type = h->out.type;
+    ops.push_back(head);
+
+    if (dalloc(h, (void **)&h->d_ops, ops.size() * sizeof(MkOp), "step phases") ||
+        dalloc(h, (void **)&h->d_bar, (size_t)wg * 128, "barrier flags") ||
+        dalloc(h, (void **)&h->d_mk_tickets, 64 * 4, "tickets") || dalloc(h, (void **)&h->d_mk_err, 4, "barrier status") ||
+        dalloc(h, (void **)&h->d_amv, (size_t)wg * 4, "argmax") || dalloc(h, (void **)&h->d_ami, (size_t)wg * 4, "argmax") ||
+        dalloc(h, (void **)&h->d_mk_part, (size_t)c.n_head * ns * (hd + 2) * 4, "attention partials"))
+        return -1;
+    if (hipMemcpy(h->d_ops, ops.data(), ops.size() * sizeof(MkOp), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(h->d_bar, 0, (size_t)wg * 128) != hipSuccess || hipMemset(h->d_mk_tickets, 0, 64 * 4) != hipSuccess ||
+        hipMemset(h->d_mk_err, 0, 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        set_err("persistent step kernel: device set-up failed");
+        return -1;
+    }
+    a.ops = h->d_ops;
+    a.part = h->d_mk_part;
+    a.bar = h->d_bar;
+    a.tickets = h->d_mk_tickets;
+    a.err = h->d_mk_err;
+    a.am_v = h->d_amv;
+    a.am_i = h->d_ami;
+    const char *pt = getenv("FORWORD_GPU_PHASE_TIMES");
+    if (pt && !strcmp(pt, "1")) {
+        if (dalloc(h, (void **)&h->d_prof, (1 + (size_t)kMkStepsPerLaunch * a.n_ops) * 8, "phase stamps")) return -1;
+        a.prof = h->d_prof;
+    }
+    h->mk_tl = tl;
+    h->mk_th = h->out.type;
+    h->mk_wg = (uint32_t)wg;
+    h->mk_lds = lds;
+    h->mk_epoch = 0;
+    h->mk = true;
     return 0;
 }
 
@@ -402,7 +555,8 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         set_err("device initialisation failed");
         FAIL();
     }
-    build_graph(h);
+    if (setup_mk(h)) FAIL();
+    if (!h->mk) build_graph(h);
 #undef FAIL
     *out = h;
     return 0;
@@ -424,7 +578,7 @@ static int step_once(forword_gpu_t *h, uint32_t token, size_t pos)
     h->h_state->n_prompt = 0;
     h->h_state->greedy = 0;
     HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
-    if (run_step(h)) return -1;
+    if (run_steps(h, 1)) return -1;
     h->traced = true;
     return 0;
 }
@@ -438,6 +592,7 @@ extern "C" float *forword_gpu_forward(forword_gpu_t *h, uint32_t token_id, size_
         set_err("forward: %s", hipGetErrorString(hipGetLastError()));
         return nullptr;
     }
+    if (mk_check(h)) return nullptr;
     return h->h_logits;
 }
 
@@ -447,6 +602,7 @@ extern "C" int forword_gpu_forward_argmax(forword_gpu_t *h, uint32_t token_id, s
     if (check_tok_pos(h, token_id, pos) || step_once(h, token_id, pos)) return -1;
     HIPCHK(hipMemcpyAsync(h->h_u32, h->d_argmax, 4, hipMemcpyDeviceToHost, h->stream), "argmax download");
     HIPCHK(hipStreamSynchronize(h->stream), "forward_argmax");
+    if (mk_check(h)) return -1;
     *next = h->h_u32[0];
     return 0;
 }
@@ -466,10 +622,10 @@ extern "C" int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *pro
     h->h_state->next = 0;
     h->h_state->greedy = 1;
     HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
-    for (size_t f = 0; f < n_fwd; f++)
-        if (run_step(h)) return -1;
+    if (run_steps(h, n_fwd)) return -1;
     if (n_gen) HIPCHK(hipMemcpyAsync(out_ids, h->d_ids, n_gen * 4, hipMemcpyDeviceToHost, h->stream), "ids download");
     HIPCHK(hipStreamSynchronize(h->stream), "generate_greedy");
+    if (mk_check(h)) return -1;
     h->h_state->pos = (uint32_t)n_fwd;     // host mirror of the device state, for forword_gpu_decode
     h->traced = true;
     return 0;
@@ -481,14 +637,14 @@ extern "C" int forword_gpu_decode(forword_gpu_t *h, size_t n_steps, uint32_t *ou
     if (!h->h_state->greedy) { set_err("decode: no greedy loop to continue (call generate_greedy first)"); return -1; }
     const size_t pos = h->h_state->pos, n_prompt = h->h_state->n_prompt;
     if (pos + n_steps > h->n_ctx) { set_err("decode: %zu more forwards exceed the KV cache (%zu)", n_steps, h->n_ctx); return -1; }
-    for (size_t i = 0; i < n_steps; i++)
-        if (run_step(h)) return -1;
+    if (run_steps(h, n_steps)) return -1;
     h->h_state->pos = (uint32_t)(pos + n_steps);
     if (out_ids && n_steps) {
         // step at position p writes the token for position p+1 at ids[p + 1 - n_prompt]
         HIPCHK(hipMemcpyAsync(out_ids, h->d_ids + (pos + 1 - n_prompt), n_steps * 4, hipMemcpyDeviceToHost, h->stream),
                "ids download");
         HIPCHK(hipStreamSynchronize(h->stream), "decode");
+        if (mk_check(h)) return -1;
     }
     return 0;
 }
@@ -536,6 +692,30 @@ extern "C" int forword_gpu_layer_trace(forword_gpu_t *h, float *out)
 
 extern "C" size_t forword_gpu_n_ctx(const forword_gpu_t *h) { return h ? h->n_ctx : 0; }
 extern "C" void *forword_gpu_stream(const forword_gpu_t *h) { return h ? (void *)h->stream : nullptr; }
+extern "C" int forword_gpu_step_impl(const forword_gpu_t *h) { return h && h->mk ? 1 : 0; }
+
+extern "C" int forword_gpu_phase_times(forword_gpu_t *h, double *us, size_t n)
+{
+    if (!h || !us) { set_err("phase_times: invalid arguments"); return -1; }
+    if (!h->d_prof || !h->prof_steps) { set_err("phase_times: no stamped persistent launch"); return -1; }
+    const size_t n_ops = h->mka.n_ops, steps = h->prof_steps;
+    std::vector<uint64_t> t(1 + steps * n_ops);
+    int dev = 0, khz = 0;
+    HIPCHK(hipStreamSynchronize(h->stream), "phase_times");
+    HIPCHK(hipMemcpy(t.data(), h->d_prof, t.size() * 8, hipMemcpyDeviceToHost), "phase_times");
+    HIPCHK(hipGetDevice(&dev), "phase_times");
+    HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev), "phase_times");
+    const size_t m = n < n_ops ? n : n_ops;
+    for (size_t i = 0; i < m; i++) {
+        double sum = 0;
+        for (size_t st = 0; st < steps; st++) {
+            const size_t k = 1 + st * n_ops + i;
+            sum += (double)(t[k] - t[k - 1]);
+        }
+        us[i] = sum / steps * 1e3 / khz;
+    }
+    return (int)m;
+}
 
 // ── operator level ───────────────────────────────────────────────────────────
 

@@ -1,0 +1,73 @@
+// Persistent token-step kernel: host-side interface (internal to libforword_gpu.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fw_kernels.h"
+
+namespace fw {
+
+// The matrices of one GEMV phase: up to three row-concatenated matrices
+// sharing one input vector (QKV), or two computed row by row together (FFN
+// gate/up).
+struct MkGemv {
+    const uint8_t *w[3];
+    uint32_t rows[3];
+    uint32_t n_rows;         // rows of the phase (QKV: sum; FFN: rows of one matrix)
+    uint32_t n_cols;
+    uint64_t row_bytes;
+    uint32_t type;
+};
+
+enum MkKind : uint32_t { MK_QKV = 0, MK_ATTN = 1, MK_WO = 2, MK_FFN = 3, MK_DOWN = 4, MK_HEAD = 5 };
+
+// One phase of the token step.  GEMV phases read input vector src (n_in
+// values; RMS-normalised with norm when set), compute g's rows and apply the
+// kind's epilogue (trace: the residual-stream row WO / DOWN record).
+struct MkOp {
+    uint32_t kind, layer, n_in, pad;
+    MkGemv g;
+    const float *norm, *src;
+    float *trace;
+};
+
+struct MkArgs {
+    const MkOp *ops;         // 5 per layer (QKV ATTN WO FFN DOWN) + HEAD
+    uint32_t n_ops, n_layer;
+    const uint8_t *embd;
+    uint32_t embd_type;
+    uint64_t embd_row_bytes;
+    float embd_scale;
+    uint32_t n_embd, n_ff, n_head, n_kv, head_dim, n_vocab, n_ctx, n_splits;
+    float eps;
+    float *kc, *vc;
+    const float *cos_tab, *sin_tab;
+    float *x, *q, *att, *h, *logits;
+    float *part;             // attention partials [n_head][n_splits][head_dim + 2]
+    StepState *state;
+    const uint32_t *prompt;
+    uint32_t *ids, *argmax_out;
+    uint32_t *bar;           // one barrier flag per workgroup, 128 bytes apart
+    uint32_t *tickets;       // n_kv attention-combine tickets + 1 argmax ticket, zero between uses
+    uint32_t *err;           // set when a barrier wait gives up
+    float *am_v;
+    uint32_t *am_i;
+    uint64_t *prof;          // optional: wall-clock stamp at kernel start, then after every phase
+    uint32_t epoch0, n_steps;
+};
+
+// Barriers one token step performs (the host advances its epoch by this much).
+inline uint32_t mk_barriers_per_step(uint32_t n_layer) { return 5 * n_layer + 1; }
+// Whether the persistent kernel supports this model (else the per-kernel path
+// runs): every layer linear of one type, Q4_0/Q5_0/Q8_0 linears and lm-head.
+bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
+                  uint32_t head_type, uint32_t embd_type);
+// Dynamic LDS of one workgroup (args fully set up, n_splits included).
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg);
+// Workgroups of one cooperative launch (one per CU), 0 if it cannot launch.
+int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes);
+hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,
+                     hipStream_t s);
+
+} // namespace fw

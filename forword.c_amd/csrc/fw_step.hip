@@ -1,0 +1,809 @@
+// Persistent token-step kernel: transformer_forward (transformer.c:149-326)
+// plus the greedy pick (sampler.c:28-32) for one or more tokens in a single
+// cooperative launch, one 512-thread workgroup per CU.
+//
+// Why: a decode step is ~4.6 GB of weight reads split over ~200 dependent
+// matrix-vector products.  As separate kernels each pays launch ramp and a
+// full memory round trip with HBM idle in between.  Here each CU keeps its
+// share of every matrix streaming: before it waits at a phase boundary, every
+// wave already has the first rows of its next phase in flight.
+//
+// Phases per layer, separated by grid barriers:
+//   QKV   input x, RMSNorm folded in; epilogue RoPE + q store + KV append
+//   ATTN  split-K over positions per KV head; the GQA group shares one read of
+//         K/V; the last workgroup to finish a head's splits combines them
+//   WO    input: attention output; epilogue x += y (+ trace row)
+//   FFN   input x, RMSNorm folded in; gate and up rows together -> silu(g)*u
+//   DOWN  input h; epilogue x += y (+ trace row)
+// then LM-HEAD (output RMSNorm folded in) with the argmax reduced by a ticket.
+//
+// GEMV mapping.  A phase's rows are split evenly (even counts, so RoPE pairs
+// stay together) over the workgroups.  Columns are cut into at most eight
+// slices of P block pairs (P a power of two); each wave owns one slice, its
+// lanes are (row-in-group, pair) = (lane / P, lane % P), so one load batch
+// covers 64/P rows.  A lane keeps the 64 input values of its pair in registers
+// for the whole phase, so a wave reads only P distinct 64-float blocks of the
+// LDS-staged input (stored with a per-block rotation of its 16-byte chunks so
+// those reads are bank-conflict free).  Per-row partial sums of the slices go
+// through LDS and are added in slice order.
+//
+// Cross-workgroup data (activations, partials, tickets, flags, step state)
+// moves through system-scope relaxed atomics: the L2s of the eight XCDs are not
+// coherent with each other and an agent-scope release writes back a whole L2.
+// K/V rows are read with plain loads: a row is written (write-through) before
+// any workgroup of the launch reads it, and caches start clean at launch.
+// Grid barriers are per-workgroup epoch flags on separate cache lines, each
+// polled by one thread of every workgroup; the spin is bounded and sets an
+// error flag, after which every workgroup leaves the kernel.  A workgroup
+// raises its flag first and then issues the next phase's first loads, so the
+// wait overlaps them.
+#include "fw_device.h"
+#include "fw_kernels.h"
+#include "fw_step.h"
+
+namespace fw {
+
+constexpr int MK_WAVES = 8;
+constexpr int MK_THREADS = MK_WAVES * 64;
+constexpr int MK_BUF = 36;                  // dwords per lane per load batch
+constexpr int MK_PART = 2 * MK_WAVES;       // LDS partials per row: [matrix][slice]
+
+// Row groups per load batch: as many block pairs as fit MK_BUF dwords.
+template <uint32_t T, int M>
+__host__ __device__ constexpr int chunk_groups()
+{
+    return MK_BUF / (M * Blk<T>::pair_dw) > 0 ? MK_BUF / (M * Blk<T>::pair_dw) : 1;
+}
+
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
+// what derives from it (slices, row ranges, trip counts) stays in SGPRs and
+// the loops over it branch uniformly.
+__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Position of input element j in the LDS staging area.
+__device__ __forceinline__ uint32_t swz(uint32_t j)
+{
+    return (j & ~63u) | ((((j >> 2) + (j >> 6)) & 15u) << 2) | (j & 3u);
+}
+
+// ── grid barrier ─────────────────────────────────────────────────────────────
+
+// Arrival: this workgroup's stores are complete (every wave waited for its own
+// memory operations), then its flag carries the new epoch.
+__device__ __forceinline__ void bar_arrive(const MkArgs &a, uint32_t epoch, uint32_t *s_fail)
+{
+    wait_mem();
+    if (threadIdx.x == 0) *s_fail = 0;
+    __syncthreads();
+    if (threadIdx.x == 0) st_sys(a.bar + blockIdx.x * 32, epoch);
+}
+
+// Wait until every workgroup's flag has reached epoch: thread t polls the flag
+// of workgroup t.  A wait that gives up (or sees another one give up) sets the
+// error word; the caller then leaves the kernel.
+__device__ __forceinline__ bool bar_wait(const MkArgs &a, uint32_t epoch, uint32_t *s_fail)
+{
+    if (threadIdx.x < gridDim.x) {
+        uint32_t spins = 0;
+        while ((int)(ld_sys(a.bar + threadIdx.x * 32) - epoch) < 0) {
+            if (++spins > (1u << 22) || ld_sys(a.err) != 0) {
+                atomicOr(a.err, 1u);
+                *s_fail = 1;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    return *s_fail == 0;
+}
+
+// ── staging ──────────────────────────────────────────────────────────────────
+
+__device__ __forceinline__ float block_sum_all(float v, float *s_red)
+{
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    __syncthreads();
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    float r = 0.f;
+#pragma unroll
+    for (int w = 0; w < MK_WAVES; w++) r += s_red[w];
+    return r;
+}
+
+// xs = (xs*w) * 1/sqrt(mean(xs^2)+eps) (rms_norm, norm.c:7-16), ss being this
+// thread's share of the sum of squares of the staged values.
+__device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *nw, float eps, float ss, float *s_red)
+{
+    ss = block_sum_all(ss, s_red);                       // also orders every thread's staging stores
+    const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
+    for (uint32_t j = threadIdx.x; j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * nw[j]) * scale;
+}
+
+// xs <- src (n floats, n even, optionally RMS-normalised), src published by
+// other workgroups: batches of 16 independent 8-byte loads per thread, so a
+// 14336-float vector costs one memory round trip instead of 28.
+__device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, const float *nw, float eps, float *s_red)
+{
+    constexpr int B = 16;
+    const uint32_t n2 = n / 2;
+    float ss = 0.f;
+    for (uint32_t j0 = threadIdx.x; j0 < n2; j0 += B * MK_THREADS) {
+        float2v v[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const uint32_t j = j0 + b * MK_THREADS;
+            if (j < n2) v[b] = ld_sys2(src + 2 * j);
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const uint32_t j = j0 + b * MK_THREADS;
+            if (j < n2) {
+                *reinterpret_cast<float2v *>(xs + swz(2 * j)) = v[b];      // 2j, 2j+1 stay adjacent
+                ss = __builtin_fmaf(v[b][0], v[b][0], ss);
+                ss = __builtin_fmaf(v[b][1], v[b][1], ss);
+            }
+        }
+    }
+    if (nw) norm_staged(xs, n, nw, eps, ss, s_red);
+    __syncthreads();
+}
+
+// ── GEMV phase ───────────────────────────────────────────────────────────────
+
+__device__ __forceinline__ uint32_t rows_per_wg(uint32_t n_rows, uint32_t n_wg)
+{
+    const uint32_t per = (n_rows + n_wg - 1) / n_wg;
+    return (per + 1) & ~1u;
+}
+
+__device__ __forceinline__ uint32_t pairs_per_slice(uint32_t n_pairs)
+{
+    const uint32_t need = (n_pairs + MK_WAVES - 1) / MK_WAVES;
+    uint32_t p = 1;
+    while (p < need) p <<= 1;
+    return p;
+}
+
+struct Map {
+    uint32_t lo, hi;          // rows of this workgroup
+    uint32_t P, S;            // pairs per slice, slices
+    uint32_t slice, wis, nws; // this wave's slice; its index among that slice's waves, their count
+    uint32_t ps, rs;          // this lane's pair in the slice, row in the group
+    uint32_t n_pairs, n_my;   // pairs per row; row groups this wave walks
+};
+
+__device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols)
+{
+    Map m;
+    const uint32_t per = rows_per_wg(n_rows, gridDim.x);
+    m.lo = min(n_rows, blockIdx.x * per);
+    m.hi = min(n_rows, m.lo + per);
+    m.n_pairs = n_cols / 64;
+    m.P = pairs_per_slice(m.n_pairs);
+    m.S = (m.n_pairs + m.P - 1) / m.P;
+    const uint32_t wave = wave_id(), lane = threadIdx.x & 63;
+    m.slice = wave % m.S;
+    m.wis = wave / m.S;
+    m.nws = MK_WAVES / m.S + (m.slice < MK_WAVES % m.S ? 1u : 0u);
+    m.ps = lane & (m.P - 1);
+    m.rs = lane / m.P;
+    const uint32_t R = 64 / m.P, n_groups = (m.hi - m.lo + R - 1) / R;
+    m.n_my = m.wis < n_groups ? (n_groups - m.wis + m.nws - 1) / m.nws : 0;
+    return m;
+}
+
+__device__ __forceinline__ uint32_t map_row(const Map &m, uint32_t k)
+{
+    return m.lo + (m.wis + k * m.nws) * (64 / m.P) + m.rs;
+}
+
+template <int M>
+__device__ __forceinline__ const uint8_t *row_ptr(const MkGemv &g, uint32_t r, int mat)
+{
+    if constexpr (M == 2) {
+        return g.w[mat] + (size_t)r * g.row_bytes;
+    } else {
+        const uint8_t *w = g.w[0];                           // constant indices only: g stays in registers
+        if (r >= g.rows[0]) {
+            r -= g.rows[0];
+            w = g.w[1];
+            if (r >= g.rows[1]) { r -= g.rows[1]; w = g.w[2]; }
+        }
+        return w + (size_t)r * g.row_bytes;
+    }
+}
+
+// Issue the loads of this wave's row groups k0 .. k0+CH-1 (needs n_my > 0).
+// Every load is issued: a group past the wave's last one, a row past the
+// workgroup's last one and a pair past the row's end are clamped to the last
+// valid one, which the caches still hold.  Without branches around the loads
+// the compiler can count them and wait only for the batch it consumes.
+template <uint32_t T, int M>
+__device__ __forceinline__ void load_chunk(const MkGemv &g, const Map &m, uint32_t k0, uint32_t (&buf)[MK_BUF])
+{
+    constexpr int NDW = Blk<T>::pair_dw, CH = chunk_groups<T, M>();
+    const uint32_t pair = min(m.slice * m.P + m.ps, m.n_pairs - 1);
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t r = min(map_row(m, min(k0 + c, m.n_my - 1)), m.hi - 1);
+#pragma unroll
+        for (int mat = 0; mat < M; mat++)
+            load_pair<T>(row_ptr<M>(g, r, mat) + (size_t)pair * (2 * Blk<T>::bytes), buf + (c * M + mat) * NDW);
+    }
+}
+
+template <uint32_t T, int M>
+__device__ __forceinline__ void prefetch(const MkGemv &g, uint32_t (&buf)[MK_BUF])
+{
+    const Map m = plan(g.n_rows, g.n_cols);
+    if (m.n_my) load_chunk<T, M>(g, m, 0, buf);
+}
+
+template <uint32_t T, int M>
+__device__ __forceinline__ void compute_chunk(const Map &m, uint32_t k0, const uint32_t (&buf)[MK_BUF],
+                                              const float (&xv)[64], float sx0, float sx1, float *part)
+{
+    constexpr int NDW = Blk<T>::pair_dw, CH = chunk_groups<T, M>();
+    const bool lane_on = m.slice * m.P + m.ps < m.n_pairs;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t k = k0 + c;
+        if (k < m.n_my) {                                    // uniform over the wave
+            const uint32_t r = map_row(m, k);
+#pragma unroll
+            for (int mat = 0; mat < M; mat++) {
+                float acc = dot_pair<T>(buf + (c * M + mat) * NDW, xv, sx0, sx1);
+                if (!lane_on || r >= m.hi) acc = 0.f;              // clamped reload
+                for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
+                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * 2 + mat) * MK_WAVES + m.slice] = acc;
+            }
+        }
+    }
+}
+
+// This workgroup's rows of g: part[(row_local*2 + matrix)*MK_WAVES + slice].
+// A holds the first batch already when have_pre.
+template <uint32_t T, int M>
+__device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *part, uint32_t (&A)[MK_BUF],
+                                     bool have_pre)
+{
+    constexpr int CH = chunk_groups<T, M>();
+    const Map m = plan(g.n_rows, g.n_cols);
+    const uint32_t pair = m.slice * m.P + m.ps;
+    float xv[64], sx0 = 0.f, sx1 = 0.f;
+    if (pair < m.n_pairs) {
+        const float *xp = xs + 64 * (size_t)pair;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = *reinterpret_cast<const float4 *>(xp + (((i + pair) & 15u) << 2));
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+        if constexpr (T != kQ8_0) {
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
+            sx0 = s0 + s1;
+            sx1 = s2 + s3;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 64; i++) xv[i] = 0.f;
+    }
+    if (m.n_my) {
+        if (!have_pre) load_chunk<T, M>(g, m, 0, A);
+        uint32_t B[MK_BUF];
+        const uint32_t n_chunks = (m.n_my + CH - 1) / CH;
+        for (uint32_t ch = 0; ch < n_chunks; ch += 2) {          // two named buffers, no copies
+            load_chunk<T, M>(g, m, (ch + 1) * CH, B);
+            compute_chunk<T, M>(m, ch * CH, A, xv, sx0, sx1, part);
+            load_chunk<T, M>(g, m, (ch + 2) * CH, A);
+            compute_chunk<T, M>(m, (ch + 1) * CH, B, xv, sx0, sx1, part);
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ float row_sum(const float *part, uint32_t rl, int mat, uint32_t n_slices)
+{
+    float y = 0.f;
+    for (uint32_t s = 0; s < n_slices; s++) y += part[(rl * 2 + mat) * MK_WAVES + s];
+    return y;
+}
+
+__device__ __forceinline__ uint32_t n_slices_of(const MkGemv &g)
+{
+    const uint32_t np = g.n_cols / 64, p = pairs_per_slice(np);
+    return (np + p - 1) / p;
+}
+
+__device__ __forceinline__ void wg_rows(uint32_t n_rows, uint32_t &lo, uint32_t &hi)
+{
+    const uint32_t per = rows_per_wg(n_rows, gridDim.x);
+    lo = min(n_rows, blockIdx.x * per);
+    hi = min(n_rows, lo + per);
+}
+
+// ── epilogues ────────────────────────────────────────────────────────────────
+
+// RoPE on q/k rows (rope.c:37-43), q store, K/V append at pos (attention.c:129-140).
+__device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const float *part, uint32_t layer, uint32_t pos)
+{
+    uint32_t lo, hi;
+    wg_rows(g.n_rows, lo, hi);
+    const uint32_t ns = n_slices_of(g), hd = a.head_dim, half = hd / 2;
+    const uint32_t kvd = a.n_kv * hd, nq = g.rows[0];
+    for (uint32_t rl = 2 * threadIdx.x; rl < hi - lo; rl += 2 * MK_THREADS) {
+        const uint32_t r = lo + rl;
+        float v0 = row_sum(part, rl, 0, ns), v1 = row_sum(part, rl + 1, 0, ns);
+        if (r < nq + kvd) {
+            const uint32_t i = ((r < nq ? r : r - nq) % hd) / 2;
+            const float c = a.cos_tab[(size_t)pos * half + i], s = a.sin_tab[(size_t)pos * half + i];
+            const float w0 = v0 * c - v1 * s, w1 = v0 * s + v1 * c;
+            v0 = w0;
+            v1 = w1;
+        }
+        float *dst;
+        if (r < nq) dst = a.q + r;
+        else if (r < nq + kvd) dst = a.kc + ((size_t)layer * a.n_ctx + pos) * kvd + (r - nq);
+        else dst = a.vc + ((size_t)layer * a.n_ctx + pos) * kvd + (r - nq - kvd);
+        st_sys(dst, v0);
+        st_sys(dst + 1, v1);
+    }
+}
+
+// x[i] += y[i] (transformer.c:271-272, 287-288) on this workgroup's rows, plus the trace row.
+__device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, const float *part, float *trace_row)
+{
+    uint32_t lo, hi;
+    wg_rows(g.n_rows, lo, hi);
+    const uint32_t ns = n_slices_of(g);
+    for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
+        const uint32_t r = lo + rl;
+        const float v = ld_sys(a.x + r) + row_sum(part, rl, 0, ns);
+        st_sys(a.x + r, v);
+        st_sys(trace_row + r, v);
+    }
+}
+
+// h = silu(gate x) * (up x) (ffn.c:82-104).
+__device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part)
+{
+    uint32_t lo, hi;
+    wg_rows(g.n_rows, lo, hi);
+    const uint32_t ns = n_slices_of(g);
+    for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS)
+        st_sys(a.h + lo + rl, silu_ref(row_sum(part, rl, 0, ns)) * row_sum(part, rl, 1, ns));
+}
+
+__device__ __forceinline__ bool am_better_mk(float v1, uint32_t i1, float v2, uint32_t i2)
+{
+    if (i1 == 0xffffffffu) return false;
+    if (i2 == 0xffffffffu) return true;
+    return v1 > v2 || (v1 == v2 && i1 < i2);
+}
+
+// Best (value, index) of the workgroup, valid in thread 0.
+__device__ __forceinline__ void block_best(float &bv, uint32_t &bi, float *s_v, uint32_t *s_i)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(bv, m, 64);
+        const uint32_t oi = __shfl_xor(bi, m, 64);
+        if (am_better_mk(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    __syncthreads();
+    if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < MK_WAVES; w++)
+            if (am_better_mk(s_v[w], s_i[w], bv, bi)) { bv = s_v[w]; bi = s_i[w]; }
+}
+
+// Logits of this workgroup's rows, their best candidate, and the winner picked
+// by the last workgroup to arrive (sampler_argmax, sampler.c:28-32: the first
+// maximum; NaN never wins; NaN at index 0 makes index 0 the answer), which also
+// advances the device-resident greedy loop (main.c:173-217).
+__device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const float *part, uint32_t pos,
+                                         uint32_t greedy, uint32_t n_prompt)
+{
+    __shared__ float s_v[MK_WAVES];
+    __shared__ uint32_t s_i[MK_WAVES];
+    __shared__ uint32_t s_last;
+    uint32_t lo, hi;
+    wg_rows(g.n_rows, lo, hi);
+    const uint32_t ns = n_slices_of(g);
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
+        const float y = row_sum(part, rl, 0, ns);
+        st_sys(a.logits + lo + rl, y);
+        if (!isnan(y) && (bi == 0xffffffffu || y > bv)) { bv = y; bi = lo + rl; }
+    }
+    wait_mem();
+    block_best(bv, bi, s_v, s_i);
+    if (threadIdx.x == 0) {
+        st_sys(a.am_v + blockIdx.x, bv);
+        st_sys(a.am_i + blockIdx.x, bi);
+        wait_mem();
+        s_last = ticket_sys(a.tickets + a.n_kv) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    bv = -INFINITY;
+    bi = 0xffffffffu;
+    for (uint32_t w = threadIdx.x; w < gridDim.x; w += MK_THREADS) {
+        const float v = ld_sys(a.am_v + w);
+        const uint32_t i = ld_sys(a.am_i + w);
+        if (am_better_mk(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    block_best(bv, bi, s_v, s_i);
+    if (threadIdx.x == 0) {
+        const uint32_t r = (bi == 0xffffffffu || isnan(ld_sys(a.logits))) ? 0u : bi;
+        st_sys(a.argmax_out, r);
+        st_sys(&a.state->next, r);
+        if (greedy) {
+            if (pos + 1 >= n_prompt) st_sys(a.ids + (pos + 1 - n_prompt), r);
+            st_sys(&a.state->token, pos + 1 < n_prompt ? a.prompt[pos + 1] : r);
+            st_sys(&a.state->pos, pos + 1);
+        }
+        st_sys(a.tickets + a.n_kv, 0u);
+    }
+}
+
+// ── attention ────────────────────────────────────────────────────────────────
+
+template <int EPL>
+__device__ __forceinline__ void load_vec(const float *p, float (&v)[EPL])
+{
+    if constexpr (EPL == 1) {
+        v[0] = *p;
+    } else if constexpr (EPL == 2) {
+        const float2 t = *reinterpret_cast<const float2 *>(p);
+        v[0] = t.x; v[1] = t.y;
+    } else {
+        const float4 t = *reinterpret_cast<const float4 *>(p);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+}
+
+// One (KV head, split) item: online softmax (log2 domain) over the split's
+// positions for the G query heads of the group (attention.c:142-164); partial
+// (o[HD], m, l) per query head to a.part.  A position is spread over 32 lanes
+// (EPL = HD/32 dimensions each), so a wave walks two positions at a time.
+template <int EPL, int G>
+__device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint32_t pos, uint32_t kvh, uint32_t split, float *lds)
+{
+    constexpr int HD = 32 * EPL;
+    float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
+    float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
+    float (*s_l)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD + MK_WAVES * G);
+    const uint32_t n_pos = pos + 1, ns = a.n_splits, chunk = (n_pos + ns - 1) / ns;
+    const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
+    const int lane = threadIdx.x & 63, wave = wave_id(), grp = lane >> 5, l32 = lane & 31;
+    const size_t kvd = (size_t)a.n_kv * HD;
+    const float *kc = a.kc + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
+    const float *vc = a.vc + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
+    const float sc = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;     // attention.c:143, in log2 units
+
+    float qv[G][EPL], m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            qv[g][e] = ld_sys(a.q + (kvh * G + g) * HD + l32 * EPL + e);
+            o[g][e] = 0.f;
+        }
+    }
+    for (uint32_t t = t0 + wave * 2 + grp; t < t1; t += 2 * MK_WAVES) {
+        float kk[EPL], vv[EPL];
+        load_vec<EPL>(kc + (size_t)t * kvd, kk);
+        load_vec<EPL>(vc + (size_t)t * kvd, vv);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[e], d);
+#pragma unroll
+            for (int o2 = 16; o2 >= 1; o2 >>= 1) d += __shfl_xor(d, o2, 64);
+            const float s = d * sc, mn = fmaxf(m[g], s);
+            const float c = exp2f(m[g] - mn), pe = exp2f(s - mn);
+            l[g] = __builtin_fmaf(l[g], c, pe);
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(o[g][e], c, pe * vv[e]);
+            m[g] = mn;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {                          // merge the wave's two position groups
+        const float mw = fmaxf(m[g], __shfl_xor(m[g], 32, 64));
+        const float c = mw == -INFINITY ? 0.f : exp2f(m[g] - mw);
+        float lw = l[g] * c;
+        lw += __shfl_xor(lw, 32, 64);
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            float ov = o[g][e] * c;
+            ov += __shfl_xor(ov, 32, 64);
+            o[g][e] = ov;
+        }
+        m[g] = mw;
+        l[g] = lw;
+    }
+    __syncthreads();                                       // LDS is free (staging / previous item)
+    if (lane < 32) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) s_o[wave][g][l32 * EPL + e] = o[g][e];
+            if (lane == 0) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * HD; i += MK_THREADS) {   // merge the eight waves
+        const int g = i / HD, dd = i % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < MK_WAVES; w++) M = fmaxf(M, s_m[w][g]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < MK_WAVES; w++) {
+            const float c = M == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+            L = __builtin_fmaf(s_l[w][g], c, L);
+            O = __builtin_fmaf(s_o[w][g][dd], c, O);
+        }
+        float *pp = a.part + ((size_t)(kvh * G + g) * ns + split) * (HD + 2);
+        st_sys(pp + dd, O);
+        if (dd == 0) { st_sys(pp + HD, M); st_sys(pp + HD + 1, L); }
+    }
+    wait_mem();
+    __syncthreads();
+}
+
+// Merge the splits of KV head kvh's G query heads into a.att.
+template <int EPL, int G>
+__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds)
+{
+    constexpr int HD = 32 * EPL;
+    const uint32_t ns = a.n_splits;
+    float *s_w = lds;                                      // [G][ns] split weights
+    float *s_inv = lds + G * ns;                           // [G] 1 / sum of weights
+    const float *base = a.part + (size_t)kvh * G * ns * (HD + 2);
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    if (wave < G) {
+        const float *pg = base + (size_t)wave * ns * (HD + 2);
+        float M = -INFINITY;
+        for (uint32_t s = lane; s < ns; s += 64) M = fmaxf(M, ld_sys(pg + (size_t)s * (HD + 2) + HD));
+        M = wave_max(M);
+        float L = 0.f;
+        for (uint32_t s = lane; s < ns; s += 64) {
+            const float ms = ld_sys(pg + (size_t)s * (HD + 2) + HD), ls = ld_sys(pg + (size_t)s * (HD + 2) + HD + 1);
+            const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+            s_w[wave * ns + s] = w;
+            L = __builtin_fmaf(ls, w, L);
+        }
+        L = wave_sum(L);
+        if (lane == 0) s_inv[wave] = 1.0f / L;
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < (uint32_t)(G * HD); i += MK_THREADS) {
+        const uint32_t g = i / HD, d = i % HD;
+        const float *pp = base + (size_t)g * ns * (HD + 2) + d;
+        const float *w = s_w + g * ns;
+        float O = 0.f;
+        for (uint32_t s0 = 0; s0 < ns; s0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = s0 + k < ns ? ld_sys(pp + (size_t)(s0 + k) * (HD + 2)) : 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (s0 + k < ns) O = __builtin_fmaf(v[k], w[s0 + k], O);
+        }
+        st_sys(a.att + (size_t)(kvh * G + g) * HD + d, O * s_inv[g]);
+    }
+    __syncthreads();
+}
+
+template <int EPL, int G>
+__device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds)
+{
+    __shared__ uint32_t s_last;
+    const uint32_t items = a.n_kv * a.n_splits;
+    for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
+        const uint32_t kvh = it % a.n_kv, split = it / a.n_kv;
+        attn_item<EPL, G>(a, layer, pos, kvh, split, lds);
+        if (threadIdx.x == 0) s_last = ticket_sys(a.tickets + kvh) == a.n_splits - 1;
+        __syncthreads();
+        if (s_last) {
+            attn_combine<EPL, G>(a, kvh, lds);
+            if (threadIdx.x == 0) st_sys(a.tickets + kvh, 0u);
+        }
+    }
+}
+
+template <int EPL>
+__device__ __forceinline__ void attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds)
+{
+    switch (a.n_head / a.n_kv) {
+    case 1: attention_t<EPL, 1>(a, layer, pos, lds); break;
+    case 2: attention_t<EPL, 2>(a, layer, pos, lds); break;
+    case 4: attention_t<EPL, 4>(a, layer, pos, lds); break;
+    default: attention_t<EPL, 8>(a, layer, pos, lds); break;
+    }
+}
+
+__device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds)
+{
+    switch (a.head_dim) {
+    case 32: attention_e<1>(a, layer, pos, lds); break;
+    case 64: attention_e<2>(a, layer, pos, lds); break;
+    default: attention_e<4>(a, layer, pos, lds); break;
+    }
+}
+
+// ── the kernel ───────────────────────────────────────────────────────────────
+
+// Embedding row (transformer.c:168-182) into the staging area, RMS-normalised
+// for the first QKV; each workgroup also publishes the residual rows it owns.
+__device__ __forceinline__ void embed(const MkArgs &a, float *xs, uint32_t tok, const float *nw, float *s_red)
+{
+    uint32_t lo, hi;
+    wg_rows(a.n_embd, lo, hi);
+    const uint8_t *row = a.embd + (size_t)tok * a.embd_row_bytes;
+    const uint32_t bb = block_bytes_dev(a.embd_type);
+    float ss = 0.f;
+    for (uint32_t j = threadIdx.x; j < a.n_embd; j += MK_THREADS) {
+        float v = a.embd_type == kF32 ? reinterpret_cast<const float *>(row)[j]
+                                      : dequant_one(row + (size_t)(j / 32) * bb, a.embd_type, j & 31);
+        if (a.embd_scale != 1.0f) v *= a.embd_scale;
+        xs[swz(j)] = v;
+        ss = __builtin_fmaf(v, v, ss);
+        if (j >= lo && j < hi) st_sys(a.x + j, v);
+    }
+    norm_staged(xs, a.n_embd, nw, a.eps, ss, s_red);
+    __syncthreads();
+}
+
+// The step is a fixed list of phases (MkOp, built once on the host) walked by
+// every workgroup; each phase ends at a grid barrier.  Phase descriptors are
+// read from memory at each phase so that no phase's operands stay live in
+// registers across the others, except the prefetched first load batch.
+// TL: type of every linear weight of the layers; TH: type of the lm-head.
+template <uint32_t TL, uint32_t TH>
+__global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
+{
+    extern __shared__ __align__(16) float lds[];
+    __shared__ float s_red[MK_WAVES];
+    __shared__ uint32_t s_fail;
+    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff;
+    float *xs = lds;
+    float *part = lds + ((n_max + 3) & ~3u);
+    uint32_t epoch = a.epoch0;
+    uint32_t pre[MK_BUF];
+    bool have_pre = false;
+    const bool stamp = a.prof && blockIdx.x == 0 && threadIdx.x == 0;
+    if (stamp) a.prof[0] = wall_clock64();
+
+    for (uint32_t step = 0; step < a.n_steps; step++) {
+        const uint32_t tok = ld_sys(&a.state->token), pos = ld_sys(&a.state->pos);
+        const uint32_t greedy = ld_sys(&a.state->greedy), n_prompt = ld_sys(&a.state->n_prompt);
+        const bool skip_head = greedy && pos + 1 < n_prompt;   // prefill: logits never read
+
+        for (uint32_t i = 0; i < a.n_ops; i++) {
+            const MkOp op = a.ops[i];                            // by value: registers, not re-read
+            const uint32_t kind = op.kind;
+            if (kind == MK_ATTN) {
+                attention(a, op.layer, pos, lds);
+            } else if (kind == MK_HEAD && skip_head) {
+                if (blockIdx.x == 0 && threadIdx.x == 0) {
+                    st_sys(&a.state->token, a.prompt[pos + 1]);
+                    st_sys(&a.state->pos, pos + 1);
+                }
+            } else {
+                if (kind == MK_QKV && op.layer == 0) embed(a, xs, tok, op.norm, s_red);
+                else stage(xs, op.src, op.n_in, op.norm, a.eps, s_red);
+                if (kind == MK_FFN) gemv<TL, 2>(op.g, xs, part, pre, have_pre);
+                else if (kind == MK_HEAD) gemv<TH, 1>(op.g, xs, part, pre, have_pre);
+                else gemv<TL, 1>(op.g, xs, part, pre, have_pre);
+                if (kind == MK_QKV) epi_qkv(a, op.g, part, op.layer, pos);
+                else if (kind == MK_FFN) epi_swiglu(a, op.g, part);
+                else if (kind == MK_HEAD) epi_head(a, op.g, part, pos, greedy, n_prompt);
+                else epi_resid(a, op.g, part, op.trace);
+            }
+            bar_arrive(a, epoch + 1, &s_fail);
+            // first load batch of the next matrix phase, in flight across the barrier
+            // (after QKV: the WO batch, held through attention)
+            if (kind != MK_ATTN) {
+                have_pre = false;
+                const MkOp *nx = nullptr;
+                if (i + 1 < a.n_ops) nx = &a.ops[a.ops[i + 1].kind == MK_ATTN ? i + 2 : i + 1];
+                else if (step + 1 < a.n_steps) nx = &a.ops[0];
+                if (nx && !(nx->kind == MK_HEAD && skip_head)) {
+                    const uint32_t nk = nx->kind;
+                    const MkGemv ng = nx->g;
+                    if (nk == MK_FFN) prefetch<TL, 2>(ng, pre);
+                    else if (nk == MK_HEAD) prefetch<TH, 1>(ng, pre);
+                    else prefetch<TL, 1>(ng, pre);
+                    have_pre = true;
+                }
+            }
+            if (!bar_wait(a, ++epoch, &s_fail)) return;
+            if (stamp) a.prof[1 + step * a.n_ops + i] = wall_clock64();
+        }
+    }
+}
+
+// ── host side ───────────────────────────────────────────────────────────────
+
+static bool mk_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
+
+bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
+                  uint32_t head_type, uint32_t embd_type)
+{
+    if (n_embd % 64 || n_ff % 64 || n_embd / 64 > 64 * MK_WAVES || n_ff / 64 > 64 * MK_WAVES) return false;
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128) return false;
+    if (group != 1 && group != 2 && group != 4 && group != 8) return false;
+    return mk_type_ok(linear_type) && mk_type_ok(head_type) && (mk_type_ok(embd_type) || embd_type == kF32);
+}
+
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg)
+{
+    auto per = [&](uint32_t rows) { uint32_t p = (rows + n_wg - 1) / n_wg; return (size_t)((p + 1) & ~1u); };
+    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff;
+    const uint32_t kvd = a.n_kv * a.head_dim;
+    size_t rows = per(a.n_vocab);
+    const size_t others[] = { per(a.n_embd + 2 * kvd), per(a.n_ff), per(a.n_embd) };
+    for (size_t r : others) rows = r > rows ? r : rows;
+    const size_t gemv_f = (((size_t)n_max + 3) & ~(size_t)3) + rows * MK_PART;
+    const size_t G = a.n_head / a.n_kv;
+    const size_t item_f = (size_t)MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G;
+    const size_t comb_f = G * a.n_splits + G;
+    size_t f = gemv_f;
+    if (item_f > f) f = item_f;
+    if (comb_f > f) f = comb_f;
+    return f * 4;
+}
+
+typedef void (*mk_kernel_t)(MkArgs);
+
+static mk_kernel_t mk_kernel(uint32_t tl, uint32_t th)
+{
+#define K(A, B) if (tl == A && th == B) return k_decode<A, B>;
+    K(kQ4_0, kQ4_0) K(kQ4_0, kQ5_0) K(kQ4_0, kQ8_0)
+    K(kQ5_0, kQ4_0) K(kQ5_0, kQ5_0) K(kQ5_0, kQ8_0)
+    K(kQ8_0, kQ4_0) K(kQ8_0, kQ5_0) K(kQ8_0, kQ8_0)
+#undef K
+    return nullptr;
+}
+
+int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes)
+{
+    mk_kernel_t k = mk_kernel(linear_type, head_type);
+    int dev = 0, per_cu = 0;
+    hipDeviceProp_t p;
+    if (!k || lds_bytes > 160 * 1024) return 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess || !p.cooperativeLaunch)
+        return 0;
+    if (hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, MK_THREADS, lds_bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    if (per_cu < 1) return 0;
+    return p.multiProcessorCount;                                  // one workgroup per CU
+}
+
+hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,
+                     hipStream_t s)
+{
+    mk_kernel_t k = mk_kernel(linear_type, head_type);
+    if (!k) return hipErrorInvalidValue;
+    MkArgs arg = a;
+    void *params[] = { &arg };
+    return hipLaunchCooperativeKernel((const void *)k, dim3(n_wg), dim3(MK_THREADS), params, (unsigned)lds_bytes, s);
+}
+
+} // namespace fw

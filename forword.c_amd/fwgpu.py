@@ -157,6 +157,8 @@ def gpu_lib():
         _sig(L, "forword_gpu_layer_trace", C.c_int, [vp, fp])
         _sig(L, "forword_gpu_n_ctx", sz, [vp])
         _sig(L, "forword_gpu_stream", vp, [vp])
+        _sig(L, "forword_gpu_step_impl", C.c_int, [vp])
+        _sig(L, "forword_gpu_phase_times", C.c_int, [vp, C.POINTER(C.c_double), sz])
         _sig(L, "forword_gpu_last_error", C.c_char_p, [])
         _sig(L, "forword_gpu_quant_matvec", C.c_int, [vp, sz, u32, vp, vp, sz, sz, vp])
         _sig(L, "forword_gpu_dequant", C.c_int, [vp, sz, u32, vp, sz, vp])
@@ -313,6 +315,21 @@ class GpuModel:
     @property
     def stream(self):
         return gpu_lib().forword_gpu_stream(self.h)
+
+    def phase_times(self) -> np.ndarray:
+        """Mean per-phase microseconds of the last persistent launch (needs
+        FORWORD_GPU_PHASE_TIMES=1 at construction)."""
+        n = 5 * self.host.cfg.n_layer + 1
+        out = np.zeros(n, np.float64)
+        got = gpu_lib().forword_gpu_phase_times(self.h, out.ctypes.data_as(C.POINTER(C.c_double)), n)
+        if got < 0:
+            raise ForwordError(f"phase_times failed: {last_error()}")
+        return out[:got]
+
+    @property
+    def persistent(self) -> bool:
+        """True when whole token steps run as one persistent kernel."""
+        return gpu_lib().forword_gpu_step_impl(self.h) == 1
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         p = gpu_lib().forword_gpu_forward(self.h, token, pos)

@@ -152,6 +152,27 @@ size_t forword_gpu_n_ctx(const forword_gpu_t *h);
 /* The hipStream_t (as void*) all of the handle's work is queued on. */
 void *forword_gpu_stream(const forword_gpu_t *h);
 
+/*
+ * Which implementation runs the token step (no counterpart in forword.c, whose
+ * step is one C function): 1 = one persistent cooperative kernel per up to 64
+ * steps (models whose layer linears share one Q4_0/Q5_0/Q8_0 type, with
+ * n_embd and n_ff multiples of 64, head_dim 32/64/128, GQA group 1/2/4/8);
+ * 0 = one kernel per phase replayed from a hipGraph.  Setting the environment
+ * variable FORWORD_GPU_MEGAKERNEL=0 before forword_gpu_init selects 0.
+ */
+int forword_gpu_step_impl(const forword_gpu_t *h);
+
+/*
+ * Profiling aid of the persistent step kernel (no counterpart in forword.c):
+ * with FORWORD_GPU_PHASE_TIMES=1 set before forword_gpu_init, the kernel
+ * stamps the wall clock after every phase.  Writes the mean duration in
+ * microseconds of each phase over the steps of the last launch into us[0..n)
+ * in step order (per layer: QKV, attention, WO, FFN, down; then the lm-head),
+ * each measured barrier to barrier, and returns the number written (-1 when
+ * nothing was stamped).
+ */
+int forword_gpu_phase_times(forword_gpu_t *h, double *us, size_t n);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *forword_gpu_last_error(void);
 

@@ -92,21 +92,27 @@ def test_kv_write_read_roundtrip_and_attention_over_written_rows():
 
 
 def test_graph_replays_match_eager():
-    """The captured step replayed many times, interleaved with eager work and
-    synchronisations, gives the same logits as direct launches."""
+    """The per-phase kernels' captured step replayed many times, interleaved
+    with eager work and synchronisations, gives the same logits as direct
+    launches."""
     m = gs.MODELS["gqa"]
     toks = [3, 99, 512, 7, 7, 800, 1, 42]
-    with fwgpu.HostModel(synth=m["spec"]()) as host:
-        with fwgpu.GpuModel(host) as gm:
-            graph_logits = [gm.forward(t, i) for i, t in enumerate(toks)]
-            replay_tokens = gm.generate_greedy(toks[:3], 6)
-        os.environ["FORWORD_GPU_GRAPH"] = "0"
-        try:
-            with fwgpu.GpuModel(host) as em:
-                eager_logits = [em.forward(t, i) for i, t in enumerate(toks)]
-                eager_tokens = em.generate_greedy(toks[:3], 6)
-        finally:
-            del os.environ["FORWORD_GPU_GRAPH"]
+    os.environ["FORWORD_GPU_MEGAKERNEL"] = "0"
+    try:
+        with fwgpu.HostModel(synth=m["spec"]()) as host:
+            with fwgpu.GpuModel(host) as gm:
+                assert not gm.persistent
+                graph_logits = [gm.forward(t, i) for i, t in enumerate(toks)]
+                replay_tokens = gm.generate_greedy(toks[:3], 6)
+            os.environ["FORWORD_GPU_GRAPH"] = "0"
+            try:
+                with fwgpu.GpuModel(host) as em:
+                    eager_logits = [em.forward(t, i) for i, t in enumerate(toks)]
+                    eager_tokens = em.generate_greedy(toks[:3], 6)
+            finally:
+                del os.environ["FORWORD_GPU_GRAPH"]
+    finally:
+        del os.environ["FORWORD_GPU_MEGAKERNEL"]
     for a, b in zip(graph_logits, eager_logits):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert np.array_equal(replay_tokens, eager_tokens)
