@@ -15,6 +15,7 @@
 namespace fw {
 
 typedef float float2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Vector types that only promise dword alignment: GGUF blocks are 18/22/34 B,

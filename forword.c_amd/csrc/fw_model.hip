@@ -105,7 +105,7 @@ struct forword_gpu {
     MkArgs mka{};
     uint32_t *d_bar = nullptr, *d_mk_err = nullptr, *d_mk_tickets = nullptr, *d_ami = nullptr;
     float *d_amv = nullptr, *d_mk_part = nullptr;
-    MkOp *d_ops = nullptr;
+    MkLayer *d_layers = nullptr;
     uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
     uint32_t prof_steps = 0;
     std::vector<void *> allocs;
@@ -312,19 +312,22 @@ static int setup_mk(forword_gpu_t *h)
         return 0;
     int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 || cus > 512) {
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 ||
+        cus > (int)kMkThreads) {
         (void)hipGetLastError();
         return 0;
     }
 
     MkArgs &a = h->mka;
     a.n_layer = L;
-    a.n_ops = 5 * L + 1;
+    a.rb_embd = h->L[0].q.row_bytes;
+    a.rb_ff = h->L[0].down.row_bytes;
+    a.head_w = h->out.w; a.head_rb = h->out.row_bytes; a.out_norm = h->out_norm;
     a.embd = h->embd.w; a.embd_type = h->embd.type; a.embd_row_bytes = h->embd.row_bytes; a.embd_scale = c.embd_scale;
     a.n_embd = n; a.n_ff = c.n_ff; a.n_head = c.n_head; a.n_kv = c.n_head_kv; a.head_dim = hd;
     a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
     a.kc = h->d_k; a.vc = h->d_v; a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
-    a.x = h->d_x; a.q = h->d_q; a.att = h->d_att; a.h = h->d_h; a.logits = h->d_logits;
+    a.x = h->d_x; a.q = h->d_q; a.att = h->d_att; a.h = h->d_h; a.logits = h->d_logits; a.trace = h->d_trace;
     a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
     // (KV head, split) attention items: about one per workgroup, >= 8 positions per split
     uint32_t ns = (uint32_t)cus / c.n_head_kv;
@@ -340,44 +343,24 @@ static int setup_mk(forword_gpu_t *h)
         return 0;
     }
 
-    std::vector<MkOp> ops;
+    std::vector<MkLayer> layers(L);
     for (uint32_t l = 0; l < L; l++) {
         const Layer &Ly = h->L[l];
-        MkOp q{}, at{}, o{}, f{}, d{};
-        q.kind = MK_QKV; q.layer = l; q.n_in = n; q.norm = Ly.attn_norm; q.src = h->d_x;
-        q.g.w[0] = Ly.q.w; q.g.w[1] = Ly.k.w; q.g.w[2] = Ly.v.w;
-        q.g.rows[0] = n; q.g.rows[1] = kvd; q.g.rows[2] = kvd; q.g.n_rows = n + 2 * kvd;
-        q.g.n_cols = n; q.g.row_bytes = Ly.q.row_bytes; q.g.type = tl;
-        at.kind = MK_ATTN; at.layer = l;
-        o.kind = MK_WO; o.layer = l; o.n_in = n; o.src = h->d_att; o.trace = h->d_trace + (size_t)(2 * l) * n;
-        o.g.w[0] = Ly.o.w; o.g.rows[0] = n; o.g.n_rows = n; o.g.n_cols = n; o.g.row_bytes = Ly.o.row_bytes; o.g.type = tl;
-        f.kind = MK_FFN; f.layer = l; f.n_in = n; f.norm = Ly.ffn_norm; f.src = h->d_x;
-        f.g.w[0] = Ly.gate.w; f.g.w[1] = Ly.up.w; f.g.rows[0] = f.g.rows[1] = c.n_ff; f.g.n_rows = c.n_ff;
-        f.g.n_cols = n; f.g.row_bytes = Ly.gate.row_bytes; f.g.type = tl;
-        d.kind = MK_DOWN; d.layer = l; d.n_in = c.n_ff; d.src = h->d_h; d.trace = h->d_trace + (size_t)(2 * l + 1) * n;
-        d.g.w[0] = Ly.down.w; d.g.rows[0] = n; d.g.n_rows = n; d.g.n_cols = c.n_ff; d.g.row_bytes = Ly.down.row_bytes;
-        d.g.type = tl;
-        for (const MkOp &op : { q, at, o, f, d }) ops.push_back(op);
+        layers[l] = MkLayer{ Ly.q.w, Ly.k.w, Ly.v.w, Ly.o.w, Ly.gate.w, Ly.up.w, Ly.down.w, Ly.attn_norm, Ly.ffn_norm };
     }
-    MkOp head{};                                     // output_norm may be absent: logits of x itself
-    head.kind = MK_HEAD; head.layer = L; head.n_in = n; head.norm = h->out_norm; head.src = h->d_x;
-    head.g.w[0] = h->out.w; head.g.rows[0] = c.n_vocab; head.g.n_rows = c.n_vocab; head.g.n_cols = n;
-    head.g.row_bytes = h->out.row_bytes; head.g.type = h->out.type;
-    ops.push_back(head);
-
-    if (dalloc(h, (void **)&h->d_ops, ops.size() * sizeof(MkOp), "step phases") ||
+    if (dalloc(h, (void **)&h->d_layers, layers.size() * sizeof(MkLayer), "layer table") ||
         dalloc(h, (void **)&h->d_bar, (size_t)wg * 128, "barrier flags") ||
         dalloc(h, (void **)&h->d_mk_tickets, 64 * 4, "tickets") || dalloc(h, (void **)&h->d_mk_err, 4, "barrier status") ||
         dalloc(h, (void **)&h->d_amv, (size_t)wg * 4, "argmax") || dalloc(h, (void **)&h->d_ami, (size_t)wg * 4, "argmax") ||
         dalloc(h, (void **)&h->d_mk_part, (size_t)c.n_head * ns * (hd + 2) * 4, "attention partials"))
         return -1;
-    if (hipMemcpy(h->d_ops, ops.data(), ops.size() * sizeof(MkOp), hipMemcpyHostToDevice) != hipSuccess ||
+    if (hipMemcpy(h->d_layers, layers.data(), layers.size() * sizeof(MkLayer), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(h->d_bar, 0, (size_t)wg * 128) != hipSuccess || hipMemset(h->d_mk_tickets, 0, 64 * 4) != hipSuccess ||
         hipMemset(h->d_mk_err, 0, 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         set_err("persistent step kernel: device set-up failed");
         return -1;
     }
-    a.ops = h->d_ops;
+    a.layers = h->d_layers;
     a.part = h->d_mk_part;
     a.bar = h->d_bar;
     a.tickets = h->d_mk_tickets;
@@ -386,7 +369,7 @@ static int setup_mk(forword_gpu_t *h)
     a.am_i = h->d_ami;
     const char *pt = getenv("FORWORD_GPU_PHASE_TIMES");
     if (pt && !strcmp(pt, "1")) {
-        if (dalloc(h, (void **)&h->d_prof, (1 + (size_t)kMkStepsPerLaunch * a.n_ops) * 8, "phase stamps")) return -1;
+        if (dalloc(h, (void **)&h->d_prof, (1 + (size_t)kMkStepsPerLaunch * (5 * L + 1)) * 8, "phase stamps")) return -1;
         a.prof = h->d_prof;
     }
     h->mk_tl = tl;
@@ -698,7 +681,7 @@ extern "C" int forword_gpu_phase_times(forword_gpu_t *h, double *us, size_t n)
 {
     if (!h || !us) { set_err("phase_times: invalid arguments"); return -1; }
     if (!h->d_prof || !h->prof_steps) { set_err("phase_times: no stamped persistent launch"); return -1; }
-    const size_t n_ops = h->mka.n_ops, steps = h->prof_steps;
+    const size_t n_ops = 5 * (size_t)h->cfg.n_layer + 1, steps = h->prof_steps;
     std::vector<uint64_t> t(1 + steps * n_ops);
     int dev = 0, khz = 0;
     HIPCHK(hipStreamSynchronize(h->stream), "phase_times");

@@ -8,9 +8,9 @@
 
 namespace fw {
 
-// The matrices of one GEMV phase: up to three row-concatenated matrices
-// sharing one input vector (QKV), or two computed row by row together (FFN
-// gate/up).
+// The matrices of one GEMV phase (built in registers): up to three
+// row-concatenated matrices sharing one input vector (QKV), or two computed
+// row by row together (FFN gate/up).
 struct MkGemv {
     const uint8_t *w[3];
     uint32_t rows[3];
@@ -22,19 +22,22 @@ struct MkGemv {
 
 enum MkKind : uint32_t { MK_QKV = 0, MK_ATTN = 1, MK_WO = 2, MK_FFN = 3, MK_DOWN = 4, MK_HEAD = 5 };
 
-// One phase of the token step.  GEMV phases read input vector src (n_in
-// values; RMS-normalised with norm when set), compute g's rows and apply the
-// kind's epilogue (trace: the residual-stream row WO / DOWN record).
-struct MkOp {
-    uint32_t kind, layer, n_in, pad;
-    MkGemv g;
-    const float *norm, *src;
-    float *trace;
+// The weights of one layer (copied into LDS at kernel start; the phase
+// descriptors are built from it in registers).
+struct MkLayer {
+    const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    const float *attn_norm, *ffn_norm;
 };
 
+// A step is 5 phases per layer (QKV ATTN WO FFN DOWN) and the lm-head (HEAD).
 struct MkArgs {
-    const MkOp *ops;         // 5 per layer (QKV ATTN WO FFN DOWN) + HEAD
-    uint32_t n_ops, n_layer;
+    const MkLayer *layers;
+    uint32_t n_layer;
+    uint64_t rb_embd;        // row bytes of a layer linear with n_embd columns
+    uint64_t rb_ff;          // row bytes of ffn_down (n_ff columns)
+    const uint8_t *head_w;   // lm-head [n_vocab rows][n_embd]
+    uint64_t head_rb;
+    const float *out_norm;   // may be null: logits of x itself
     const uint8_t *embd;
     uint32_t embd_type;
     uint64_t embd_row_bytes;
@@ -44,6 +47,7 @@ struct MkArgs {
     float *kc, *vc;
     const float *cos_tab, *sin_tab;
     float *x, *q, *att, *h, *logits;
+    float *trace;            // [2 * n_layer][n_embd] residual stream after each residual add
     float *part;             // attention partials [n_head][n_splits][head_dim + 2]
     StepState *state;
     const uint32_t *prompt;
@@ -56,6 +60,10 @@ struct MkArgs {
     uint64_t *prof;          // optional: wall-clock stamp at kernel start, then after every phase
     uint32_t epoch0, n_steps;
 };
+
+// Threads of one workgroup; each barrier flag is polled by one thread, so a
+// launch has at most this many workgroups.
+constexpr uint32_t kMkThreads = 256;
 
 // Barriers one token step performs (the host advances its epoch by this much).
 inline uint32_t mk_barriers_per_step(uint32_t n_layer) { return 5 * n_layer + 1; }

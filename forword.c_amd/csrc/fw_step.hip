@@ -43,10 +43,12 @@
 
 namespace fw {
 
-constexpr int MK_WAVES = 8;
+constexpr int MK_WAVES = 4;                 // one wave per SIMD: 512 registers (VGPR + AGPR) each
 constexpr int MK_THREADS = MK_WAVES * 64;
+static_assert(MK_THREADS == (int)kMkThreads, "workgroup size");
 constexpr int MK_BUF = 36;                  // dwords per lane per load batch
-constexpr int MK_PART = 2 * MK_WAVES;       // LDS partials per row: [matrix][slice]
+constexpr int MK_SMAX = 8;                  // column slices per row at most (64 block pairs each)
+constexpr int MK_PART = 2 * MK_SMAX;        // LDS partials per row: [matrix][slice]
 
 // Row groups per load batch: as many block pairs as fit MK_BUF dwords.
 template <uint32_t T, int M>
@@ -118,29 +120,61 @@ __device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *
 {
     ss = block_sum_all(ss, s_red);                       // also orders every thread's staging stores
     const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
-    for (uint32_t j = threadIdx.x; j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * nw[j]) * scale;
+    const FW_GLOBAL float *w = gptr(nw);
+    for (uint32_t j = threadIdx.x; j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * w[j]) * scale;
 }
 
-// xs <- src (n floats, n even, optionally RMS-normalised), src published by
-// other workgroups: batches of 16 independent 8-byte loads per thread, so a
-// 14336-float vector costs one memory round trip instead of 28.
+// xs <- src (n floats, n even, optionally RMS-normalised by weights nw), src
+// published by other workgroups.  The loads go out in batches (8-byte
+// system-scope loads for src, plain loads for nw in the same batch), so
+// staging costs one memory round trip per batch.
 __device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, const float *nw, float eps, float *s_red)
 {
     constexpr int B = 16;
     const uint32_t n2 = n / 2;
-    float ss = 0.f;
-    for (uint32_t j0 = threadIdx.x; j0 < n2; j0 += B * MK_THREADS) {
-        float2v v[B];
+    if (nw && n2 <= B * MK_THREADS) {                    // one batch: x and its norm weights together
+        const FW_GLOBAL float2v *w2 = reinterpret_cast<const FW_GLOBAL float2v *>(gptr(nw));
+        float2v v[B], w[B];
 #pragma unroll
         for (int b = 0; b < B; b++) {
+            const uint32_t j = threadIdx.x + b * MK_THREADS;
+            if (j < n2) { v[b] = ld_sys2(src + 2 * j); w[b] = w2[j]; }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int b = 0; b < B; b++)
+            if (threadIdx.x + b * MK_THREADS < n2) {
+                ss = __builtin_fmaf(v[b][0], v[b][0], ss);
+                ss = __builtin_fmaf(v[b][1], v[b][1], ss);
+            }
+        ss = block_sum_all(ss, s_red);
+        const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const uint32_t j = threadIdx.x + b * MK_THREADS;
+            if (j < n2) {
+                float2v o;
+                o[0] = (v[b][0] * w[b][0]) * scale;
+                o[1] = (v[b][1] * w[b][1]) * scale;
+                *reinterpret_cast<float2v *>(xs + swz(2 * j)) = o;           // 2j, 2j+1 stay adjacent
+            }
+        }
+        __syncthreads();
+        return;
+    }
+    float ss = 0.f;
+    for (uint32_t j0 = threadIdx.x; j0 < n2; j0 += 2 * B * MK_THREADS) {
+        float2v v[2 * B];
+#pragma unroll
+        for (int b = 0; b < 2 * B; b++) {
             const uint32_t j = j0 + b * MK_THREADS;
             if (j < n2) v[b] = ld_sys2(src + 2 * j);
         }
 #pragma unroll
-        for (int b = 0; b < B; b++) {
+        for (int b = 0; b < 2 * B; b++) {
             const uint32_t j = j0 + b * MK_THREADS;
             if (j < n2) {
-                *reinterpret_cast<float2v *>(xs + swz(2 * j)) = v[b];      // 2j, 2j+1 stay adjacent
+                *reinterpret_cast<float2v *>(xs + swz(2 * j)) = v[b];
                 ss = __builtin_fmaf(v[b][0], v[b][0], ss);
                 ss = __builtin_fmaf(v[b][1], v[b][1], ss);
             }
@@ -152,7 +186,8 @@ __device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, c
 
 // ── GEMV phase ───────────────────────────────────────────────────────────────
 
-__device__ __forceinline__ uint32_t rows_per_wg(uint32_t n_rows, uint32_t n_wg)
+// Rows of a phase per workgroup: an even count, so RoPE pairs stay together.
+__host__ __device__ inline uint32_t mk_rows_per_wg(uint32_t n_rows, uint32_t n_wg)
 {
     const uint32_t per = (n_rows + n_wg - 1) / n_wg;
     return (per + 1) & ~1u;
@@ -162,31 +197,42 @@ __device__ __forceinline__ uint32_t pairs_per_slice(uint32_t n_pairs)
 {
     const uint32_t need = (n_pairs + MK_WAVES - 1) / MK_WAVES;
     uint32_t p = 1;
-    while (p < need) p <<= 1;
+    while (p < need && p < 64) p <<= 1;
     return p;
 }
 
 struct Map {
     uint32_t lo, hi;          // rows of this workgroup
-    uint32_t P, S;            // pairs per slice, slices
-    uint32_t slice, wis, nws; // this wave's slice; its index among that slice's waves, their count
+    uint32_t P, S;            // pairs per slice, slices (<= MK_SMAX)
+    uint32_t slice, sstep;    // this wave's first slice and the stride to its next one
+    uint32_t wis, nws;        // this wave's index among its slice's waves, their count
     uint32_t ps, rs;          // this lane's pair in the slice, row in the group
-    uint32_t n_pairs, n_my;   // pairs per row; row groups this wave walks
+    uint32_t n_pairs, n_my;   // pairs per row; row groups this wave walks per slice
 };
 
+// Fewer slices than waves: several waves share a slice and split its row
+// groups.  More slices than waves: each wave walks slices wave, wave + 4, ...
 __device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols)
 {
     Map m;
-    const uint32_t per = rows_per_wg(n_rows, gridDim.x);
+    const uint32_t per = mk_rows_per_wg(n_rows, gridDim.x);
     m.lo = min(n_rows, blockIdx.x * per);
     m.hi = min(n_rows, m.lo + per);
     m.n_pairs = n_cols / 64;
     m.P = pairs_per_slice(m.n_pairs);
     m.S = (m.n_pairs + m.P - 1) / m.P;
     const uint32_t wave = wave_id(), lane = threadIdx.x & 63;
-    m.slice = wave % m.S;
-    m.wis = wave / m.S;
-    m.nws = MK_WAVES / m.S + (m.slice < MK_WAVES % m.S ? 1u : 0u);
+    if (m.S <= (uint32_t)MK_WAVES) {
+        m.slice = wave % m.S;
+        m.sstep = MK_SMAX;
+        m.wis = wave / m.S;
+        m.nws = MK_WAVES / m.S + (m.slice < MK_WAVES % m.S ? 1u : 0u);
+    } else {
+        m.slice = wave;
+        m.sstep = MK_WAVES;
+        m.wis = 0;
+        m.nws = 1;
+    }
     m.ps = lane & (m.P - 1);
     m.rs = lane / m.P;
     const uint32_t R = 64 / m.P, n_groups = (m.hi - m.lo + R - 1) / R;
@@ -257,49 +303,53 @@ __device__ __forceinline__ void compute_chunk(const Map &m, uint32_t k0, const u
                 float acc = dot_pair<T>(buf + (c * M + mat) * NDW, xv, sx0, sx1);
                 if (!lane_on || r >= m.hi) acc = 0.f;              // clamped reload
                 for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
-                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * 2 + mat) * MK_WAVES + m.slice] = acc;
+                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * 2 + mat) * MK_SMAX + m.slice] = acc;
             }
         }
     }
 }
 
-// This workgroup's rows of g: part[(row_local*2 + matrix)*MK_WAVES + slice].
-// A holds the first batch already when have_pre.
+// This workgroup's rows of g: part[(row_local*2 + matrix)*MK_SMAX + slice].
+// A holds the first batch of the wave's first slice already when have_pre.
 template <uint32_t T, int M>
 __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *part, uint32_t (&A)[MK_BUF],
                                      bool have_pre)
 {
     constexpr int CH = chunk_groups<T, M>();
-    const Map m = plan(g.n_rows, g.n_cols);
-    const uint32_t pair = m.slice * m.P + m.ps;
-    float xv[64], sx0 = 0.f, sx1 = 0.f;
-    if (pair < m.n_pairs) {
-        const float *xp = xs + 64 * (size_t)pair;
+    Map m = plan(g.n_rows, g.n_cols);
+    for (uint32_t sl = m.slice; sl < m.S; sl += m.sstep) {
+        const bool pre_ok = have_pre && sl == m.slice;
+        m.slice = sl;
+        const uint32_t pair = sl * m.P + m.ps;
+        float xv[64], sx0 = 0.f, sx1 = 0.f;
+        if (pair < m.n_pairs) {
+            const float *xp = xs + 64 * (size_t)pair;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float4 v = *reinterpret_cast<const float4 *>(xp + (((i + pair) & 15u) << 2));
-            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            for (int i = 0; i < 16; i++) {
+                const float4 v = *reinterpret_cast<const float4 *>(xp + (((i + pair) & 15u) << 2));
+                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            }
+            if constexpr (T != kQ8_0) {
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
+                sx0 = s0 + s1;
+                sx1 = s2 + s3;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 64; i++) xv[i] = 0.f;
         }
-        if constexpr (T != kQ8_0) {
-            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
-            sx0 = s0 + s1;
-            sx1 = s2 + s3;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 64; i++) xv[i] = 0.f;
-    }
-    if (m.n_my) {
-        if (!have_pre) load_chunk<T, M>(g, m, 0, A);
-        uint32_t B[MK_BUF];
-        const uint32_t n_chunks = (m.n_my + CH - 1) / CH;
-        for (uint32_t ch = 0; ch < n_chunks; ch += 2) {          // two named buffers, no copies
-            load_chunk<T, M>(g, m, (ch + 1) * CH, B);
-            compute_chunk<T, M>(m, ch * CH, A, xv, sx0, sx1, part);
-            load_chunk<T, M>(g, m, (ch + 2) * CH, A);
-            compute_chunk<T, M>(m, (ch + 1) * CH, B, xv, sx0, sx1, part);
+        if (m.n_my) {
+            if (!pre_ok) load_chunk<T, M>(g, m, 0, A);
+            uint32_t B[MK_BUF];
+            const uint32_t n_chunks = (m.n_my + CH - 1) / CH;
+            for (uint32_t ch = 0; ch < n_chunks; ch += 2) {          // two named buffers, no copies
+                load_chunk<T, M>(g, m, (ch + 1) * CH, B);
+                compute_chunk<T, M>(m, ch * CH, A, xv, sx0, sx1, part);
+                load_chunk<T, M>(g, m, (ch + 2) * CH, A);
+                compute_chunk<T, M>(m, (ch + 1) * CH, B, xv, sx0, sx1, part);
+            }
         }
     }
     __syncthreads();
@@ -308,7 +358,7 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
 __device__ __forceinline__ float row_sum(const float *part, uint32_t rl, int mat, uint32_t n_slices)
 {
     float y = 0.f;
-    for (uint32_t s = 0; s < n_slices; s++) y += part[(rl * 2 + mat) * MK_WAVES + s];
+    for (uint32_t s = 0; s < n_slices; s++) y += part[(rl * 2 + mat) * MK_SMAX + s];
     return y;
 }
 
@@ -320,15 +370,17 @@ __device__ __forceinline__ uint32_t n_slices_of(const MkGemv &g)
 
 __device__ __forceinline__ void wg_rows(uint32_t n_rows, uint32_t &lo, uint32_t &hi)
 {
-    const uint32_t per = rows_per_wg(n_rows, gridDim.x);
+    const uint32_t per = mk_rows_per_wg(n_rows, gridDim.x);
     lo = min(n_rows, blockIdx.x * per);
     hi = min(n_rows, lo + per);
 }
 
 // ── epilogues ────────────────────────────────────────────────────────────────
 
-// RoPE on q/k rows (rope.c:37-43), q store, K/V append at pos (attention.c:129-140).
-__device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const float *part, uint32_t layer, uint32_t pos)
+// RoPE on q/k rows (rope.c:37-43) with this position's cos/sin (rope[0..hd/2)
+// and rope[hd/2..hd) in LDS), q store, K/V append at pos (attention.c:129-140).
+__device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const float *part, const float *rope,
+                                        uint32_t layer, uint32_t pos)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
@@ -339,7 +391,7 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
         float v0 = row_sum(part, rl, 0, ns), v1 = row_sum(part, rl + 1, 0, ns);
         if (r < nq + kvd) {
             const uint32_t i = ((r < nq ? r : r - nq) % hd) / 2;
-            const float c = a.cos_tab[(size_t)pos * half + i], s = a.sin_tab[(size_t)pos * half + i];
+            const float c = rope[i], s = rope[half + i];
             const float w0 = v0 * c - v1 * s, w1 = v0 * s + v1 * c;
             v0 = w0;
             v1 = w1;
@@ -353,18 +405,32 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
     }
 }
 
-// x[i] += y[i] (transformer.c:271-272, 287-288) on this workgroup's rows, plus the trace row.
-__device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, const float *part, float *trace_row)
+// x[i] += y[i] (transformer.c:271-272, 287-288) on this workgroup's rows: the
+// workgroup keeps its own rows of x in LDS (x_own), publishes the sums and
+// records the trace row.
+__device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, const float *part, float *x_own,
+                                          float *trace_row)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices_of(g);
     for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
         const uint32_t r = lo + rl;
-        const float v = ld_sys(a.x + r) + row_sum(part, rl, 0, ns);
+        const float v = x_own[rl] + row_sum(part, rl, 0, ns);
+        x_own[rl] = v;
         st_sys(a.x + r, v);
         st_sys(trace_row + r, v);
     }
+}
+
+// apply_silu (ffn.c:17-25) with the reference's two branches, in float
+// arithmetic (expf, within an ulp or two of the correctly rounded value).
+__device__ __forceinline__ float silu_f(float v)
+{
+    float sig;
+    if (v >= 0.0f) sig = 1.0f / (1.0f + expf(-v));
+    else { const float e = expf(v); sig = e / (1.0f + e); }
+    return v * sig;
 }
 
 // h = silu(gate x) * (up x) (ffn.c:82-104).
@@ -374,7 +440,7 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices_of(g);
     for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS)
-        st_sys(a.h + lo + rl, silu_ref(row_sum(part, rl, 0, ns)) * row_sum(part, rl, 1, ns));
+        st_sys(a.h + lo + rl, silu_f(row_sum(part, rl, 0, ns)) * row_sum(part, rl, 1, ns));
 }
 
 __device__ __forceinline__ bool am_better_mk(float v1, uint32_t i1, float v2, uint32_t i2)
@@ -456,16 +522,16 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
 // ── attention ────────────────────────────────────────────────────────────────
 
 template <int EPL>
-__device__ __forceinline__ void load_vec(const float *p, float (&v)[EPL])
+__device__ __forceinline__ void load_vec(const FW_GLOBAL float *p, float (&v)[EPL])
 {
     if constexpr (EPL == 1) {
         v[0] = *p;
     } else if constexpr (EPL == 2) {
-        const float2 t = *reinterpret_cast<const float2 *>(p);
-        v[0] = t.x; v[1] = t.y;
+        const float2v t = *reinterpret_cast<const FW_GLOBAL float2v *>(p);
+        v[0] = t[0]; v[1] = t[1];
     } else {
-        const float4 t = *reinterpret_cast<const float4 *>(p);
-        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        const float4v t = *reinterpret_cast<const FW_GLOBAL float4v *>(p);
+        v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
     }
 }
 
@@ -484,8 +550,8 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
     const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
     const int lane = threadIdx.x & 63, wave = wave_id(), grp = lane >> 5, l32 = lane & 31;
     const size_t kvd = (size_t)a.n_kv * HD;
-    const float *kc = a.kc + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
-    const float *vc = a.vc + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
+    const FW_GLOBAL float *kc = gptr(a.kc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
+    const FW_GLOBAL float *vc = gptr(a.vc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
     const float sc = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;     // attention.c:143, in log2 units
 
     float qv[G][EPL], m[G], l[G], o[G][EPL];
@@ -499,23 +565,33 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
             o[g][e] = 0.f;
         }
     }
-    for (uint32_t t = t0 + wave * 2 + grp; t < t1; t += 2 * MK_WAVES) {
-        float kk[EPL], vv[EPL];
-        load_vec<EPL>(kc + (size_t)t * kvd, kk);
-        load_vec<EPL>(vc + (size_t)t * kvd, vv);
+    // two positions per lane group per iteration, both loads issued first; the
+    // second one past the split's end reloads the first and is given no weight
+    for (uint32_t t = t0 + wave * 2 + grp; t < t1; t += 4 * MK_WAVES) {
+        const bool has2 = t + 2 * MK_WAVES < t1;
+        const uint32_t t2 = has2 ? t + 2 * MK_WAVES : t;
+        float kk[2][EPL], vv[2][EPL];
+        load_vec<EPL>(kc + (size_t)t * kvd, kk[0]);
+        load_vec<EPL>(vc + (size_t)t * kvd, vv[0]);
+        load_vec<EPL>(kc + (size_t)t2 * kvd, kk[1]);
+        load_vec<EPL>(vc + (size_t)t2 * kvd, vv[1]);
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float d = 0.f;
+        for (int u = 0; u < 2; u++) {
 #pragma unroll
-            for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[e], d);
+            for (int g = 0; g < G; g++) {
+                float d = 0.f;
 #pragma unroll
-            for (int o2 = 16; o2 >= 1; o2 >>= 1) d += __shfl_xor(d, o2, 64);
-            const float s = d * sc, mn = fmaxf(m[g], s);
-            const float c = exp2f(m[g] - mn), pe = exp2f(s - mn);
-            l[g] = __builtin_fmaf(l[g], c, pe);
+                for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[u][e], d);
 #pragma unroll
-            for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(o[g][e], c, pe * vv[e]);
-            m[g] = mn;
+                for (int o2 = 16; o2 >= 1; o2 >>= 1) d += __shfl_xor(d, o2, 64);
+                const float s = (u == 0 || has2) ? d * sc : -INFINITY;     // m[g] is finite after u = 0
+                const float mn = fmaxf(m[g], s);
+                const float c = exp2f(m[g] - mn), pe = exp2f(s - mn);
+                l[g] = __builtin_fmaf(l[g], c, pe);
+#pragma unroll
+                for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(o[g][e], c, pe * vv[u][e]);
+                m[g] = mn;
+            }
         }
     }
 #pragma unroll
@@ -563,30 +639,37 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
     __syncthreads();
 }
 
-// Merge the splits of KV head kvh's G query heads into a.att.
+// Merge the splits of KV head kvh's G query heads into a.att: every split's
+// (m, l) in one batch of loads, then each thread's o values in batches of 32.
 template <int EPL, int G>
 __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds)
 {
-    constexpr int HD = 32 * EPL;
+    constexpr int HD = 32 * EPL, SB = 32;
     const uint32_t ns = a.n_splits;
-    float *s_w = lds;                                      // [G][ns] split weights
-    float *s_inv = lds + G * ns;                           // [G] 1 / sum of weights
-    const float *base = a.part + (size_t)kvh * G * ns * (HD + 2);
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    if (wave < G) {
-        const float *pg = base + (size_t)wave * ns * (HD + 2);
+    float *s_w = lds;                                      // [G][ns] m, then the split weights
+    float *s_l = lds + G * ns;                             // [G][ns] l
+    float *s_inv = lds + 2 * G * ns;                       // [G] 1 / sum of weights
+    const float *base = a.part + (size_t)kvh * G * ns * (HD + 2);   // (head g, split s) at (g*ns + s)*(HD+2)
+    for (uint32_t t = threadIdx.x; t < G * ns; t += MK_THREADS) {
+        const float2v ml = ld_sys2(base + (size_t)t * (HD + 2) + HD);
+        s_w[t] = ml[0];
+        s_l[t] = ml[1];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    for (uint32_t g = wave_id(); g < (uint32_t)G; g += MK_WAVES) {
         float M = -INFINITY;
-        for (uint32_t s = lane; s < ns; s += 64) M = fmaxf(M, ld_sys(pg + (size_t)s * (HD + 2) + HD));
+        for (uint32_t s = lane; s < ns; s += 64) M = fmaxf(M, s_w[g * ns + s]);
         M = wave_max(M);
         float L = 0.f;
         for (uint32_t s = lane; s < ns; s += 64) {
-            const float ms = ld_sys(pg + (size_t)s * (HD + 2) + HD), ls = ld_sys(pg + (size_t)s * (HD + 2) + HD + 1);
+            const float ms = s_w[g * ns + s];
             const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-            s_w[wave * ns + s] = w;
-            L = __builtin_fmaf(ls, w, L);
+            s_w[g * ns + s] = w;
+            L = __builtin_fmaf(s_l[g * ns + s], w, L);
         }
         L = wave_sum(L);
-        if (lane == 0) s_inv[wave] = 1.0f / L;
+        if (lane == 0) s_inv[g] = 1.0f / L;
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < (uint32_t)(G * HD); i += MK_THREADS) {
@@ -594,12 +677,12 @@ __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, floa
         const float *pp = base + (size_t)g * ns * (HD + 2) + d;
         const float *w = s_w + g * ns;
         float O = 0.f;
-        for (uint32_t s0 = 0; s0 < ns; s0 += 8) {
-            float v[8];
+        for (uint32_t s0 = 0; s0 < ns; s0 += SB) {
+            float v[SB];
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = s0 + k < ns ? ld_sys(pp + (size_t)(s0 + k) * (HD + 2)) : 0.f;
+            for (int k = 0; k < SB; k++) v[k] = s0 + k < ns ? ld_sys(pp + (size_t)(s0 + k) * (HD + 2)) : 0.f;
 #pragma unroll
-            for (int k = 0; k < 8; k++)
+            for (int k = 0; k < SB; k++)
                 if (s0 + k < ns) O = __builtin_fmaf(v[k], w[s0 + k], O);
         }
         st_sys(a.att + (size_t)(kvh * G + g) * HD + d, O * s_inv[g]);
@@ -646,9 +729,87 @@ __device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint3
 
 // ── the kernel ───────────────────────────────────────────────────────────────
 
+// LDS layout of one workgroup, in floats (host and device agree on it).
+struct MkLds {
+    uint32_t part;            // GEMV per-row slice partials (after the staged input xs at 0)
+    uint32_t tab;             // the layer table (MkLayer[n_layer])
+    uint32_t x_own;           // this workgroup's rows of x
+    uint32_t rope;            // cos (head_dim/2) then sin (head_dim/2) of the current position
+    uint32_t total;
+};
+
+__host__ __device__ inline MkLds mk_layout(const MkArgs &a, uint32_t n_wg)
+{
+    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff, kvd = a.n_kv * a.head_dim;
+    uint32_t rows = mk_rows_per_wg(a.n_vocab, n_wg);
+    const uint32_t others[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg), mk_rows_per_wg(a.n_ff, n_wg),
+                                mk_rows_per_wg(a.n_embd, n_wg) };
+    for (uint32_t r : others) rows = r > rows ? r : rows;
+    const uint32_t G = a.n_head / a.n_kv;
+    MkLds L;
+    L.part = (n_max + 3) & ~3u;
+    uint32_t region = L.part + rows * MK_PART;                               // GEMV phases
+    const uint32_t item = MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G;      // attention item
+    const uint32_t comb = 2 * G * a.n_splits + G;                           // attention combine
+    region = region > item ? region : item;
+    region = region > comb ? region : comb;
+    L.tab = (region + 3) & ~3u;
+    L.x_own = L.tab + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4);
+    L.rope = L.x_own + mk_rows_per_wg(a.n_embd, n_wg);
+    L.total = L.rope + a.head_dim;
+    return L;
+}
+
+// A pointer read from LDS, made wave-uniform (scalar registers).
+template <typename T> __device__ __forceinline__ T *uni(T *p)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+
+// The matrices of phase `kind` of `layer`.
+__device__ __forceinline__ MkGemv phase_gemv(const MkArgs &a, const MkLayer *tab, uint32_t kind, uint32_t layer)
+{
+    MkGemv g{};
+    g.n_cols = a.n_embd;
+    g.row_bytes = a.rb_embd;
+    if (kind == MK_HEAD) {
+        g.w[0] = a.head_w;
+        g.rows[0] = g.n_rows = a.n_vocab;
+        g.row_bytes = a.head_rb;
+        return g;
+    }
+    const MkLayer &L = tab[layer];
+    const uint32_t kvd = a.n_kv * a.head_dim;
+    if (kind == MK_QKV) {
+        g.w[0] = uni(L.wq); g.w[1] = uni(L.wk); g.w[2] = uni(L.wv);
+        g.rows[0] = a.n_embd; g.rows[1] = g.rows[2] = kvd;
+        g.n_rows = a.n_embd + 2 * kvd;
+    } else if (kind == MK_WO) {
+        g.w[0] = uni(L.wo);
+        g.rows[0] = g.n_rows = a.n_embd;
+    } else if (kind == MK_FFN) {
+        g.w[0] = uni(L.wg); g.w[1] = uni(L.wu);
+        g.rows[0] = g.rows[1] = g.n_rows = a.n_ff;
+    } else {
+        g.w[0] = uni(L.wd);
+        g.rows[0] = g.n_rows = a.n_embd;
+        g.n_cols = a.n_ff;
+        g.row_bytes = a.rb_ff;
+    }
+    return g;
+}
+
+__device__ __forceinline__ uint32_t phase_kind(const MkArgs &a, uint32_t i)
+{
+    return i == 5 * a.n_layer ? (uint32_t)MK_HEAD : i % 5;
+}
+
 // Embedding row (transformer.c:168-182) into the staging area, RMS-normalised
-// for the first QKV; each workgroup also publishes the residual rows it owns.
-__device__ __forceinline__ void embed(const MkArgs &a, float *xs, uint32_t tok, const float *nw, float *s_red)
+// for the first QKV; the workgroup's own rows also go to x_own and x.
+__device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, uint32_t tok, const float *nw,
+                                      float *s_red)
 {
     uint32_t lo, hi;
     wg_rows(a.n_embd, lo, hi);
@@ -661,16 +822,19 @@ __device__ __forceinline__ void embed(const MkArgs &a, float *xs, uint32_t tok, 
         if (a.embd_scale != 1.0f) v *= a.embd_scale;
         xs[swz(j)] = v;
         ss = __builtin_fmaf(v, v, ss);
-        if (j >= lo && j < hi) st_sys(a.x + j, v);
+        if (j >= lo && j < hi) {
+            x_own[j - lo] = v;
+            st_sys(a.x + j, v);
+        }
     }
     norm_staged(xs, a.n_embd, nw, a.eps, ss, s_red);
     __syncthreads();
 }
 
-// The step is a fixed list of phases (MkOp, built once on the host) walked by
-// every workgroup; each phase ends at a grid barrier.  Phase descriptors are
-// read from memory at each phase so that no phase's operands stay live in
-// registers across the others, except the prefetched first load batch.
+// Every workgroup walks the step's phases (5 per layer + the lm-head), each
+// ending at a grid barrier.  Descriptors are built in registers from the layer
+// table in LDS; the only state carried across a barrier in registers is the
+// next matrix phase's first load batch.
 // TL: type of every linear weight of the layers; TH: type of the lm-head.
 template <uint32_t TL, uint32_t TH>
 __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
@@ -678,52 +842,67 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     extern __shared__ __align__(16) float lds[];
     __shared__ float s_red[MK_WAVES];
     __shared__ uint32_t s_fail;
-    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff;
-    float *xs = lds;
-    float *part = lds + ((n_max + 3) & ~3u);
+    const MkLds lay = mk_layout(a, gridDim.x);
+    float *xs = lds, *part = lds + lay.part, *x_own = lds + lay.x_own, *rope = lds + lay.rope;
+    MkLayer *tab = reinterpret_cast<MkLayer *>(lds + lay.tab);
+    {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.layers);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(tab);
+        for (uint32_t j = threadIdx.x; j < a.n_layer * (uint32_t)(sizeof(MkLayer) / 4); j += MK_THREADS) dst[j] = src[j];
+    }
+    const uint32_t n_ops = 5 * a.n_layer + 1, half = a.head_dim / 2;
     uint32_t epoch = a.epoch0;
     uint32_t pre[MK_BUF];
     bool have_pre = false;
     const bool stamp = a.prof && blockIdx.x == 0 && threadIdx.x == 0;
     if (stamp) a.prof[0] = wall_clock64();
+    __syncthreads();
 
     for (uint32_t step = 0; step < a.n_steps; step++) {
         const uint32_t tok = ld_sys(&a.state->token), pos = ld_sys(&a.state->pos);
         const uint32_t greedy = ld_sys(&a.state->greedy), n_prompt = ld_sys(&a.state->n_prompt);
         const bool skip_head = greedy && pos + 1 < n_prompt;   // prefill: logits never read
+        for (uint32_t t = threadIdx.x; t < half; t += MK_THREADS) {
+            rope[t] = a.cos_tab[(size_t)pos * half + t];
+            rope[half + t] = a.sin_tab[(size_t)pos * half + t];
+        }
 
-        for (uint32_t i = 0; i < a.n_ops; i++) {
-            const MkOp op = a.ops[i];                            // by value: registers, not re-read
-            const uint32_t kind = op.kind;
+        for (uint32_t i = 0; i < n_ops; i++) {
+            const uint32_t kind = phase_kind(a, i), layer = i / 5;
             if (kind == MK_ATTN) {
-                attention(a, op.layer, pos, lds);
+                attention(a, layer, pos, lds);
             } else if (kind == MK_HEAD && skip_head) {
                 if (blockIdx.x == 0 && threadIdx.x == 0) {
                     st_sys(&a.state->token, a.prompt[pos + 1]);
                     st_sys(&a.state->pos, pos + 1);
                 }
             } else {
-                if (kind == MK_QKV && op.layer == 0) embed(a, xs, tok, op.norm, s_red);
-                else stage(xs, op.src, op.n_in, op.norm, a.eps, s_red);
-                if (kind == MK_FFN) gemv<TL, 2>(op.g, xs, part, pre, have_pre);
-                else if (kind == MK_HEAD) gemv<TH, 1>(op.g, xs, part, pre, have_pre);
-                else gemv<TL, 1>(op.g, xs, part, pre, have_pre);
-                if (kind == MK_QKV) epi_qkv(a, op.g, part, op.layer, pos);
-                else if (kind == MK_FFN) epi_swiglu(a, op.g, part);
-                else if (kind == MK_HEAD) epi_head(a, op.g, part, pos, greedy, n_prompt);
-                else epi_resid(a, op.g, part, op.trace);
+                // one call site per GEMV variant keeps the executed code small
+                const float *src = kind == MK_WO ? a.att : kind == MK_DOWN ? a.h : a.x;
+                const uint32_t n_in = kind == MK_DOWN ? a.n_ff : a.n_embd;
+                const float *nw = kind == MK_QKV ? uni(tab[layer].attn_norm)
+                                : kind == MK_FFN ? uni(tab[layer].ffn_norm)
+                                : kind == MK_HEAD ? a.out_norm : nullptr;
+                if (kind == MK_QKV && layer == 0) embed(a, xs, x_own, tok, nw, s_red);
+                else stage(xs, src, n_in, nw, a.eps, s_red);
+                const MkGemv g = phase_gemv(a, tab, kind, layer);
+                if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, pre, have_pre);
+                else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, pre, have_pre);
+                else gemv<TL, 1>(g, xs, part, pre, have_pre);
+                if (kind == MK_QKV) epi_qkv(a, g, part, rope, layer, pos);
+                else if (kind == MK_FFN) epi_swiglu(a, g, part);
+                else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
+                else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd);
             }
             bar_arrive(a, epoch + 1, &s_fail);
             // first load batch of the next matrix phase, in flight across the barrier
-            // (after QKV: the WO batch, held through attention)
-            if (kind != MK_ATTN) {
-                have_pre = false;
-                const MkOp *nx = nullptr;
-                if (i + 1 < a.n_ops) nx = &a.ops[a.ops[i + 1].kind == MK_ATTN ? i + 2 : i + 1];
-                else if (step + 1 < a.n_steps) nx = &a.ops[0];
-                if (nx && !(nx->kind == MK_HEAD && skip_head)) {
-                    const uint32_t nk = nx->kind;
-                    const MkGemv ng = nx->g;
+            // (none before attention: its registers are needed there)
+            have_pre = false;
+            const bool wrap = i + 1 == n_ops;
+            if (!wrap || step + 1 < a.n_steps) {
+                const uint32_t ni = wrap ? 0 : i + 1, nk = phase_kind(a, ni);
+                if (nk != MK_ATTN && !(nk == MK_HEAD && skip_head)) {
+                    const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
                     if (nk == MK_FFN) prefetch<TL, 2>(ng, pre);
                     else if (nk == MK_HEAD) prefetch<TH, 1>(ng, pre);
                     else prefetch<TL, 1>(ng, pre);
@@ -731,7 +910,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 }
             }
             if (!bar_wait(a, ++epoch, &s_fail)) return;
-            if (stamp) a.prof[1 + step * a.n_ops + i] = wall_clock64();
+            if (stamp) a.prof[1 + step * n_ops + i] = wall_clock64();
         }
     }
 }
@@ -743,29 +922,13 @@ static bool mk_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8
 bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
                   uint32_t head_type, uint32_t embd_type)
 {
-    if (n_embd % 64 || n_ff % 64 || n_embd / 64 > 64 * MK_WAVES || n_ff / 64 > 64 * MK_WAVES) return false;
+    if (n_embd % 64 || n_ff % 64 || n_embd / 64 > 64 * MK_SMAX || n_ff / 64 > 64 * MK_SMAX) return false;
     if (head_dim != 32 && head_dim != 64 && head_dim != 128) return false;
     if (group != 1 && group != 2 && group != 4 && group != 8) return false;
     return mk_type_ok(linear_type) && mk_type_ok(head_type) && (mk_type_ok(embd_type) || embd_type == kF32);
 }
 
-size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg)
-{
-    auto per = [&](uint32_t rows) { uint32_t p = (rows + n_wg - 1) / n_wg; return (size_t)((p + 1) & ~1u); };
-    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff;
-    const uint32_t kvd = a.n_kv * a.head_dim;
-    size_t rows = per(a.n_vocab);
-    const size_t others[] = { per(a.n_embd + 2 * kvd), per(a.n_ff), per(a.n_embd) };
-    for (size_t r : others) rows = r > rows ? r : rows;
-    const size_t gemv_f = (((size_t)n_max + 3) & ~(size_t)3) + rows * MK_PART;
-    const size_t G = a.n_head / a.n_kv;
-    const size_t item_f = (size_t)MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G;
-    const size_t comb_f = G * a.n_splits + G;
-    size_t f = gemv_f;
-    if (item_f > f) f = item_f;
-    if (comb_f > f) f = comb_f;
-    return f * 4;
-}
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg) { return (size_t)mk_layout(a, n_wg).total * 4; }
 
 typedef void (*mk_kernel_t)(MkArgs);
 

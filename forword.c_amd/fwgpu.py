@@ -138,12 +138,14 @@ def host_lib():
 
 
 def gpu_lib():
-    """Load lib/libforword_gpu.so; raises when it is missing (no CPU fallback exists)."""
+    """Load lib/libforword_gpu.so (or the build named by FORWORD_GPU_LIB, for A/B
+    comparisons of kernel variants); raises when it is missing (no CPU fallback exists)."""
     global _gpu
     if _gpu is None:
-        if not os.path.exists(GPU_LIB):
-            raise RuntimeError(f"{GPU_LIB} is not built (run __graft_entry__.build())")
-        L = C.CDLL(GPU_LIB)
+        path = os.environ.get("FORWORD_GPU_LIB", GPU_LIB)
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+        L = C.CDLL(path)
         _sig(L, "forword_gpu_init", C.c_int, [C.POINTER(vp), vp, sz, C.POINTER(TensorDesc), sz,
                                                C.POINTER(Config), sz, fp, fp])
         _sig(L, "forword_gpu_free", None, [vp])
