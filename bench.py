@@ -1,15 +1,27 @@
 #!/usr/bin/env python3
-"""Decode benchmark of the forword MI355X path: Llama-3-8B-shaped random-init
-Q4_0 GGUF (Q8_0 embedding/output), 512-token random prompt, then greedy decode
-at positions 512..767.  One step = one token forward (transformer_forward) plus
-the greedy pick, run device-resident through the C ABI.
+"""Decode benchmark of the forword MI355X path.
+
+Default workload: Llama-3-8B-shaped random-init GGUF (Q4_0 linears, Q8_0
+embedding/output), 512-token random prompt, then greedy decode at positions
+528..783 (after 16 warm-up steps).  One step = one token forward
+(transformer_forward) plus the greedy pick, run device-resident through the
+C ABI; the persistent step kernel runs up to 64 steps per launch.
 
 Prints one JSON line:
   value        decode tok/s (weights and KV already in HBM)
-  roofline     the dominant kernel (fused gate/up Q4_0 GEMV + SiLU*up, 54% of each
-               layer's weight bytes) timed with HIP events over >= 1 GiB of
-               rotating weight copies; achieved = algorithmic bytes / duration
+  roofline     the dominant kernel (the persistent step kernel, all of the
+               decode time): algorithmic bytes of the steps one launch runs
+               (weights + embedding row + norm weights + KV read/write) over
+               its mean duration, timed with HIP events on the handle's stream
+  microbench   quant_matvec GB/s per weight type and shape (>= 1 GiB of
+               rotating weight copies so the 256 MB last-level cache cannot
+               serve repeats)
   cpu_baseline the oracle (CPU restatement of forword.c) on one core, bounded sample
+
+Other modes: --config lc (8B shape at 32K context, KV rows 0..32767 written
+with N(0,1) through kv_write, then greedy decode), --config 70b, --mode decode
+(just the timed decode, for profilers), --mode copy (device-to-device copy of
+known size: calibrates the memory-traffic counters).
 """
 from __future__ import annotations
 
@@ -28,6 +40,7 @@ import fwgpu  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "decode tok/s (8B-shape Q4_0, 1 GPU) + quant-matvec HBM GB/s % of peak"
+STEPS_PER_LAUNCH = 64
 
 
 def log(msg):
@@ -35,7 +48,7 @@ def log(msg):
 
 
 class Hip:
-    """The few HIP runtime calls the timing needs (events on a given stream)."""
+    """The few HIP runtime calls the timing needs (events on a given stream, D2D copy)."""
 
     def __init__(self):
         fwgpu.gpu_lib()   # loads libamdhip64 as a dependency
@@ -50,8 +63,8 @@ class Hip:
         fwgpu._sig(L, "hipEventRecord", C.c_int, [C.c_void_p, C.c_void_p])
         fwgpu._sig(L, "hipEventSynchronize", C.c_int, [C.c_void_p])
         fwgpu._sig(L, "hipEventElapsedTime", C.c_int, [C.POINTER(C.c_float), C.c_void_p, C.c_void_p])
-        fwgpu._sig(L, "hipEventDestroy", C.c_int, [C.c_void_p])
         fwgpu._sig(L, "hipStreamSynchronize", C.c_int, [C.c_void_p])
+        fwgpu._sig(L, "hipMemcpyAsync", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p])
 
     def event(self):
         e = C.c_void_p()
@@ -72,8 +85,8 @@ class Hip:
 
 
 def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34):
-    """Algorithmic bytes of one token step at position pos: weights, embedding row,
-    norm weights, KV read (rows 0..pos incl. the one just written) and KV write."""
+    """Algorithmic bytes of one token step at position pos: weights, embedding row, norm
+    weights, KV read (rows 0..pos incl. the one just written) and KV write."""
     n, ff, L, hd, kv = cfg.n_embd, cfg.n_ff, cfg.n_layer, cfg.head_dim, cfg.n_head_kv
     lin = L * ((n // 32) * linear_bb * (2 * n + 2 * kv * hd + 2 * ff) + (ff // 32) * linear_bb * n)
     head = (n // 32) * out_bb * cfg.n_vocab
@@ -83,33 +96,62 @@ def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34):
     return lin + head + embd + norms + kvb
 
 
-def time_dominant_kernel(hip, stream, n_in, n_ff, reps_min=64):
-    """Fused gate/up Q4_0 GEMV at the layer shape, cycling through >= 1 GiB of
-    distinct weight copies so the 256 MB last-level cache cannot serve repeats."""
-    per = fwgpu.BLOCK_BYTES[fwgpu.GGML_Q4_0] * (n_in // 32) * n_ff
-    copies = max(2, -(-(1 << 30) // (2 * per)))
-    w = fwgpu.synth_matrix(fwgpu.GGML_Q4_0, n_ff, n_in, seed=123)
-    bufs = [(fwgpu.DeviceBuffer.from_array(w), fwgpu.DeviceBuffer.from_array(w)) for _ in range(copies)]
-    x = fwgpu.DeviceBuffer.from_array(fwgpu.randn(7, n_in))
-    h = fwgpu.DeviceBuffer(n_ff * 4)
-    reps = max(reps_min, 2 * copies)
-    for i in range(copies):                                  # warm-up pass
-        fwgpu.ops.ffn_swiglu(bufs[i][0], bufs[i][1], fwgpu.GGML_Q4_0, x, h, n_in, n_ff, stream, sync=False)
+def timed_decode(hip, gm, steps):
+    """Continue the greedy loop for `steps` steps in launches of STEPS_PER_LAUNCH, each
+    bracketed by HIP events on the handle's stream.  Returns (total ms, [(ms, n)])."""
+    stream = gm.stream
+    launches = []
+    done = 0
     hip.sync(stream)
-    ev = [hip.event() for _ in range(reps + 1)]
-    for i in range(reps):
-        hip.record(ev[i], stream)
-        g, u = bufs[i % copies]
-        fwgpu.ops.ffn_swiglu(g, u, fwgpu.GGML_Q4_0, x, h, n_in, n_ff, stream, sync=False)
-    hip.record(ev[reps], stream)
+    t_start = hip.event()
+    hip.record(t_start, stream)
+    while done < steps:
+        n = min(STEPS_PER_LAUNCH, steps - done)
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, stream)
+        gm.decode(n, copy_out=False)
+        hip.record(e1, stream)
+        launches.append((e0, e1, n))
+        done += n
+    t_end = hip.event()
+    hip.record(t_end, stream)
     hip.sync(stream)
-    per_launch = [hip.ms(ev[i], ev[i + 1]) for i in range(reps)]
-    total = hip.ms(ev[0], ev[reps])
-    for b in bufs:
-        b[0].free()
-        b[1].free()
-    algo = 2 * per + 4 * n_in + 4 * n_ff
-    return algo, float(np.mean(per_launch)), total / reps, copies
+    total = hip.ms(t_start, t_end)
+    return total, [(hip.ms(a, b), n) for a, b, n in launches]
+
+
+def microbench(hip, min_bytes=1 << 30, reps=48):
+    """quant_matvec (operator entry point) GB/s at the microbenchmark shapes."""
+    L = fwgpu.gpu_lib()
+    out = []
+    x = fwgpu.DeviceBuffer.from_array(fwgpu.randn(7, 14336))
+    y = fwgpu.DeviceBuffer(14336 * 4)
+    for t in (fwgpu.GGML_Q4_0, fwgpu.GGML_Q5_0, fwgpu.GGML_Q8_0):
+        for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
+            w = fwgpu.synth_matrix(t, rows, cols, seed=100 + t)
+            copies = max(2, -(-min_bytes // w.nbytes))
+            bufs = [fwgpu.DeviceBuffer.from_array(w) for _ in range(copies)]
+            algo = w.nbytes + 4 * cols + 4 * rows
+            for i in range(copies):                                 # warm-up pass
+                assert L.forword_gpu_quant_matvec(bufs[i].ptr, w.nbytes, t, x.ptr, y.ptr, cols, rows, None) == 0
+            hip.sync(None)
+            ev = [hip.event() for _ in range(reps + 1)]
+            for i in range(reps):
+                hip.record(ev[i], None)
+                assert L.forword_gpu_quant_matvec(bufs[i % copies].ptr, w.nbytes, t, x.ptr, y.ptr,
+                                                  cols, rows, None) == 0
+            hip.record(ev[reps], None)
+            hip.sync(None)
+            us = float(np.mean([hip.ms(ev[i], ev[i + 1]) for i in range(reps)])) * 1e3
+            for b in bufs:
+                b.free()
+            gbs = algo / (us * 1e-6) / 1e9
+            out.append({"type": fwgpu.TYPE_NAMES[t], "rows": rows, "cols": cols, "bytes": algo,
+                        "us": round(us, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"microbench {fwgpu.TYPE_NAMES[t]} {rows}x{cols}: {us:.2f} us, {gbs:.0f} GB/s")
+    x.free()
+    y.free()
+    return out
 
 
 def cpu_baseline(host, budget_s):
@@ -130,25 +172,45 @@ def cpu_baseline(host, budget_s):
     return done / el, done, el
 
 
+def copy_calibration(hip, mb):
+    """Device-to-device copies of a known size, for memory-counter calibration."""
+    n = mb << 20
+    a, b = fwgpu.DeviceBuffer(n), fwgpu.DeviceBuffer(n)
+    for _ in range(3):
+        assert hip.L.hipMemcpyAsync(b.ptr, a.ptr, n, 3, None) == 0
+    hip.sync(None)
+    print(json.dumps({"copy_bytes": n, "copies": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--config", default="8b", choices=["8b", "70b", "tiny"])
+    ap.add_argument("--config", default="8b", choices=["8b", "lc", "70b", "tiny"])
+    ap.add_argument("--mode", default="full", choices=["full", "decode", "copy"])
+    ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-microbench", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this decode path runs on one GPU; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    hip = Hip()
+    if args.mode == "copy":
+        copy_calibration(hip, args.copy_mb)
+        return
 
-    n_ctx = args.prompt + args.warmup + args.steps + 1
-    if args.config == "8b":
+    lc = args.config == "lc"
+    lc_pos = 32768
+    n_ctx = (lc_pos if lc else args.prompt) + args.warmup + args.steps + 1
+    if args.config in ("8b", "lc"):
         sp = fwgpu.spec_8b(n_ctx=max(768, n_ctx))
-        workload = "Llama-3-8B-shape Q4_0 greedy decode (Q8_0 embedding/output)"
+        workload = ("Llama-3-8B-shape Q4_0 greedy decode at 32K context (Q8_0 embedding/output)" if lc else
+                    "Llama-3-8B-shape Q4_0 greedy decode (Q8_0 embedding/output)")
     elif args.config == "70b":
         sp = fwgpu.spec_70b(n_ctx=max(384, n_ctx))
         workload = "Llama-3-70B-shape Q4_0 greedy decode (Q8_0 embedding/output)"
@@ -159,67 +221,108 @@ def main():
     t0 = time.perf_counter()
     host = fwgpu.HostModel(synth=sp, max_ctx=n_ctx)
     log(f"model generated in {time.perf_counter() - t0:.1f}s ({host.data_size / 1e9:.2f} GB of tensors)")
-    hip = Hip()
     t0 = time.perf_counter()
     gm = fwgpu.GpuModel(host)
-    step_impl = "persistent kernel" if gm.persistent else "per-phase kernels (hipGraph)"
+    gm_persistent = gm.persistent
+    step_impl = "persistent kernel" if gm_persistent else "per-phase kernels (hipGraph)"
     log(f"uploaded to HBM in {time.perf_counter() - t0:.1f}s; token step: {step_impl}")
-    stream = gm.stream
-    prompt = np.random.default_rng(512).integers(3, host.cfg.n_vocab, args.prompt).astype(np.uint32)
+    cfg = host.cfg
 
-    t0 = time.perf_counter()
-    first = gm.generate_greedy(prompt, 1)
-    prefill_s = time.perf_counter() - t0
-    log(f"prefill {args.prompt} tokens (token-by-token, as the reference) in {prefill_s:.2f}s")
-    gm.decode(args.warmup)
-    hip.sync(stream)
-    e0, e1 = hip.event(), hip.event()
-    hip.record(e0, stream)
-    gm.decode(args.steps, copy_out=False)
-    hip.record(e1, stream)
-    hip.sync(stream)
-    ms = hip.ms(e0, e1)
-    tok_s = args.steps / (ms / 1e3)
-    p0 = args.prompt + args.warmup
-    avg_bytes = float(np.mean([step_bytes(host.cfg, p) for p in range(p0, p0 + args.steps)]))
-    log(f"decode: {args.steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s, "
-        f"{avg_bytes * tok_s / 1e9:.0f} GB/s effective")
+    first, prefill_s = None, None
+    if lc:
+        # KV rows 0..lc_pos-1 of every layer from N(0,1), written through kv_write
+        kvd = cfg.n_head_kv * cfg.head_dim
+        rng = np.random.default_rng(4)
+        t0 = time.perf_counter()
+        chunk = 4096
+        kbuf = rng.standard_normal((chunk, kvd), dtype=np.float32)
+        vbuf = rng.standard_normal((chunk, kvd), dtype=np.float32)
+        for layer in range(cfg.n_layer):
+            for c0 in range(0, lc_pos, chunk):
+                sh = (layer * 131 + c0) % chunk
+                gm.kv_write(layer, c0, np.roll(kbuf, sh, axis=0), np.roll(vbuf, sh, axis=0))
+        log(f"KV rows 0..{lc_pos - 1} of {cfg.n_layer} layers written in {time.perf_counter() - t0:.1f}s")
+        gm.decode_from(7, lc_pos, args.warmup)
+        p0 = lc_pos + args.warmup
+    else:
+        prompt = np.random.default_rng(512).integers(3, cfg.n_vocab, args.prompt).astype(np.uint32)
+        t0 = time.perf_counter()
+        first = gm.generate_greedy(prompt, 1)
+        prefill_s = time.perf_counter() - t0
+        log(f"prefill {args.prompt} tokens (token-by-token, as the reference) in {prefill_s:.2f}s")
+        gm.decode(args.warmup)
+        p0 = args.prompt + args.warmup
+    hip.sync(gm.stream)
+
+    total_ms, launches = timed_decode(hip, gm, args.steps)
+    tok_s = args.steps / (total_ms / 1e3)
+    byte_list = [step_bytes(cfg, p) for p in range(p0, p0 + args.steps)]
+    avg_bytes = float(np.mean(byte_list))
+    log(f"decode: {args.steps} steps at positions {p0}..{p0 + args.steps - 1} in {total_ms:.2f} ms "
+        f"-> {tok_s:.1f} tok/s, {avg_bytes * tok_s / 1e9:.0f} GB/s effective")
+    if args.mode == "decode":
+        print(json.dumps({"tok_s": round(tok_s, 2), "steps": args.steps, "ms": round(total_ms, 3)}), flush=True)
+        return
     if gm.persistent and os.environ.get("FORWORD_GPU_PHASE_TIMES") == "1":
-        pt, L = gm.phase_times(), host.cfg.n_layer
+        pt, L = gm.phase_times(), cfg.n_layer
         names = ["qkv", "attn", "wo", "ffn", "down"]
         per = {nm: float(np.mean(pt[i:5 * L:5])) for i, nm in enumerate(names)}
         log("phase us (mean over layers, last launch): " + ", ".join(f"{k} {v:.2f}" for k, v in per.items())
             + f", head {pt[-1]:.2f}; step {pt.sum():.1f}")
 
-    algo, dur_ms, dur_ms_total, copies = time_dominant_kernel(hip, stream, host.cfg.n_embd, host.cfg.n_ff)
-    achieved = algo / (dur_ms / 1e3) / 1e9
-    log(f"dominant kernel: {algo} B per launch, {dur_ms * 1e3:.2f} us avg -> {achieved:.0f} GB/s")
+    # roofline of the dominant kernel: the full-size launches of the timed decode
+    n_l = max(n for _, n in launches)
+    i0, per_bytes, per_ms = 0, [], []
+    for ms, n in launches:
+        if n == n_l:
+            per_bytes.append(sum(byte_list[i0:i0 + n]))
+            per_ms.append(ms)
+        i0 += n
+    launch_bytes = float(np.mean(per_bytes))
+    launch_ms = float(np.mean(per_ms))
+    achieved = launch_bytes / (launch_ms / 1e3) / 1e9
+    log(f"persistent launch: {n_l} steps, {launch_bytes / 1e9:.2f} GB, {launch_ms:.2f} ms -> {achieved:.0f} GB/s")
+
+    micro = None
+    if not args.no_microbench and args.config == "8b":
+        micro = microbench(hip)
     gm.close()
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and args.config == "8b":
         v, n, el = cpu_baseline(host, args.cpu_seconds)
         cpu = {"value": round(v, 4), "unit": "tok/s", "cores": 1, "kind": "port",
                "sample": f"{n} forwards of the same model at positions 0..{n - 1}, 1 thread, "
                          f"{el:.1f} s (oracle/fw_cpu.c: forword.c's fp32 order, Q4_0 added)"}
     host.close()
 
+    cfg_out = {"workload": workload, "step_impl": step_impl,
+               "decode_positions": [p0, p0 + args.steps - 1], "kv_cache": "fp32 in HBM",
+               "step_bytes_avg": int(avg_bytes), "step_gbs": round(avg_bytes * tok_s / 1e9, 1),
+               "step_roofline_frac": round(avg_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
+    if lc:
+        cfg_out["kv_prefill"] = f"rows 0..{lc_pos - 1} N(0,1) via forword_gpu_kv_write"
+    else:
+        cfg_out["prompt_tokens"] = args.prompt
+        cfg_out["prefill_tok_s"] = round(args.prompt / prefill_s, 1)
+        cfg_out["first_token"] = int(first[0])
+    traffic, traffic_src = None, None
+    tf = os.path.join(ROOT, "profiles", "k_decode_8b_q4_0_traffic.json")
+    if args.config == "8b" and gm_persistent and os.path.exists(tf):
+        # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE runs of this workload
+        t = json.load(open(tf))
+        traffic, traffic_src = t["traffic_bytes_per_launch"], t["source"]
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4),
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded random-init GGUF, random prompt ids)",
-        "config": {"workload": workload, "prompt_tokens": args.prompt, "step_impl": step_impl,
-                   "decode_positions": [p0, p0 + args.steps - 1], "kv_cache": "fp32 in HBM",
-                   "step_bytes_avg": int(avg_bytes), "step_gbs": round(avg_bytes * tok_s / 1e9, 1),
-                   "step_roofline_frac": round(avg_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
-                   "prefill_tok_s": round(args.prompt / prefill_s, 1), "first_token": int(first[0])},
+        "config": cfg_out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_qmv<Q4_0, SWIGLU> (fused gate/up GEMV + SiLU*up), "
-                               f"{host.cfg.n_ff}x{host.cfg.n_embd} x2, {copies} rotating copies",
-                     "bytes_per_launch": algo, "avg_us": round(dur_ms * 1e3, 3),
-                     "avg_us_back_to_back": round(dur_ms_total * 1e3, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": f"k_decode (persistent token step, {n_l} steps per launch)",
+                     "bytes_per_launch": int(launch_bytes), "avg_ms_per_launch": round(launch_ms, 3)},
+        "microbench": micro,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -632,6 +632,30 @@ extern "C" int forword_gpu_decode(forword_gpu_t *h, size_t n_steps, uint32_t *ou
     return 0;
 }
 
+extern "C" int forword_gpu_decode_from(forword_gpu_t *h, uint32_t token, size_t pos, size_t n_steps,
+                                       uint32_t *out_ids)
+{
+    if (!h || !n_steps) { set_err("decode_from: invalid arguments"); return -1; }
+    if (check_tok_pos(h, token, pos)) return -1;
+    if (pos + n_steps > h->n_ctx) { set_err("decode_from: %zu forwards from %zu exceed the KV cache (%zu)", n_steps, pos, h->n_ctx); return -1; }
+    // n_prompt = pos + 1: no prefill step, ids[0] is the token for position pos + 1
+    h->h_state->token = token;
+    h->h_state->pos = (uint32_t)pos;
+    h->h_state->n_prompt = (uint32_t)(pos + 1);
+    h->h_state->next = 0;
+    h->h_state->greedy = 1;
+    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    if (run_steps(h, n_steps)) return -1;
+    h->h_state->pos = (uint32_t)(pos + n_steps);
+    h->traced = true;
+    if (out_ids) {
+        HIPCHK(hipMemcpyAsync(out_ids, h->d_ids, n_steps * 4, hipMemcpyDeviceToHost, h->stream), "ids download");
+        HIPCHK(hipStreamSynchronize(h->stream), "decode_from");
+        if (mk_check(h)) return -1;
+    }
+    return 0;
+}
+
 static int kv_args(forword_gpu_t *h, size_t layer, size_t pos0, size_t n_pos)
 {
     if (!h) { set_err("NULL handle"); return -1; }

@@ -153,6 +153,7 @@ def gpu_lib():
         _sig(L, "forword_gpu_forward_argmax", C.c_int, [vp, u32, sz, u32p])
         _sig(L, "forword_gpu_generate_greedy", C.c_int, [vp, u32p, sz, sz, u32p])
         _sig(L, "forword_gpu_decode", C.c_int, [vp, sz, u32p])
+        _sig(L, "forword_gpu_decode_from", C.c_int, [vp, u32, sz, sz, u32p])
         _sig(L, "forword_gpu_ffn_swiglu", C.c_int, [vp, vp, sz, u32, vp, vp, sz, sz, vp])
         _sig(L, "forword_gpu_kv_write", C.c_int, [vp, sz, sz, sz, fp, fp])
         _sig(L, "forword_gpu_kv_read", C.c_int, [vp, sz, sz, sz, fp, fp])
@@ -360,6 +361,13 @@ class GpuModel:
         out = np.zeros(n_steps, np.uint32) if copy_out else None
         _check(gpu_lib().forword_gpu_decode(self.h, n_steps, out.ctypes.data_as(u32p) if copy_out else None),
                "decode")
+        return out
+
+    def decode_from(self, token: int, pos: int, n_steps: int, copy_out: bool = True):
+        """Greedy loop entered at (token, pos), e.g. after a kv_write prefill."""
+        out = np.zeros(n_steps, np.uint32) if copy_out else None
+        _check(gpu_lib().forword_gpu_decode_from(self.h, token, pos, n_steps,
+                                                 out.ctypes.data_as(u32p) if copy_out else None), "decode_from")
         return out
 
     def kv_write(self, layer: int, pos0: int, k: np.ndarray | None, v: np.ndarray | None):

@@ -129,6 +129,16 @@ int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *prompt, size_t
 int forword_gpu_decode(forword_gpu_t *h, size_t n_steps, uint32_t *out_ids);
 
 /*
+ * Start a greedy loop at an arbitrary position: forward `token` at `pos` and
+ * continue for n_steps forwards in all, each fed the previous argmax
+ * (main.c:173-217 entered after a prefill done by other means, e.g.
+ * forword_gpu_kv_write of rows [0, pos)).  Composition of transformer_forward
+ * and sampler_argmax with no single counterpart in forword.c.  out_ids as in
+ * forword_gpu_decode; forword_gpu_decode may continue the loop afterwards.
+ */
+int forword_gpu_decode_from(forword_gpu_t *h, uint32_t token, size_t pos, size_t n_steps, uint32_t *out_ids);
+
+/*
  * Write / read rows of the device KV cache for one layer: positions
  * [pos0, pos0+n_pos), each row n_head_kv*head_dim floats, K post-RoPE
  * (kv_k/kv_v, kv_cache.h:45-51; the append in attention.c:135-140).
