@@ -303,7 +303,7 @@ static int setup_mk(forword_gpu_t *h)
     const char *env = getenv("FORWORD_GPU_MEGAKERNEL");
     if (env && !strcmp(env, "0")) return 0;
     const forword_gpu_config_t &c = h->cfg;
-    const uint32_t n = c.n_embd, hd = c.head_dim, kvd = c.n_head_kv * hd, L = c.n_layer;
+    const uint32_t n = c.n_embd, hd = c.head_dim, L = c.n_layer;
     const uint32_t tl = h->L[0].q.type;
     for (const Layer &Ly : h->L)
         for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })
@@ -313,7 +313,7 @@ static int setup_mk(forword_gpu_t *h)
     int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 ||
-        cus > (int)kMkThreads) {
+        cus > (int)kMkPollers) {
         (void)hipGetLastError();
         return 0;
     }
@@ -336,8 +336,8 @@ static int setup_mk(forword_gpu_t *h)
     if (ns > 256) ns = 256;
     if (ns < 1) ns = 1;
     a.n_splits = ns;
-    const size_t lds = mk_lds_bytes(a, (uint32_t)cus);
-    const int wg = mk_max_workgroups(tl, h->out.type, lds);
+    const size_t lds = mk_lds_bytes(a, (uint32_t)cus, tl, h->out.type);
+    const int wg = lds ? mk_max_workgroups(tl, h->out.type, lds) : 0;
     if (wg != cus) {
         fprintf(stderr, "forword_gpu: persistent step kernel cannot launch (LDS %zu B); using per-phase kernels\n", lds);
         return 0;

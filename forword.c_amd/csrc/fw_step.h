@@ -61,9 +61,10 @@ struct MkArgs {
     uint32_t epoch0, n_steps;
 };
 
-// Threads of one workgroup; each barrier flag is polled by one thread, so a
-// launch has at most this many workgroups.
-constexpr uint32_t kMkThreads = 256;
+// Threads of one workgroup, and how many of them poll barrier flags and load
+// staged inputs (one flag each, so a launch has at most kMkPollers workgroups).
+constexpr uint32_t kMkThreads = 512;
+constexpr uint32_t kMkPollers = 256;
 
 // Barriers one token step performs (the host advances its epoch by this much).
 inline uint32_t mk_barriers_per_step(uint32_t n_layer) { return 5 * n_layer + 1; }
@@ -71,8 +72,9 @@ inline uint32_t mk_barriers_per_step(uint32_t n_layer) { return 5 * n_layer + 1;
 // runs): every layer linear of one type, Q4_0/Q5_0/Q8_0 linears and lm-head.
 bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
                   uint32_t head_type, uint32_t embd_type);
-// Dynamic LDS of one workgroup (args fully set up, n_splits included).
-size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg);
+// Dynamic LDS of one workgroup (args fully set up, n_splits included), 0 if
+// the staged input, the partials and weight rings of every phase do not fit.
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type);
 // Workgroups of one cooperative launch (one per CU), 0 if it cannot launch.
 int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes);
 hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,

@@ -1,12 +1,14 @@
 // Persistent token-step kernel: transformer_forward (transformer.c:149-326)
 // plus the greedy pick (sampler.c:28-32) for one or more tokens in a single
-// cooperative launch, one 512-thread workgroup per CU.
+// cooperative launch, one 512-thread workgroup (8 waves) per CU.
 //
 // Why: a decode step is ~4.6 GB of weight reads split over ~200 dependent
 // matrix-vector products.  As separate kernels each pays launch ramp and a
 // full memory round trip with HBM idle in between.  Here each CU keeps its
-// share of every matrix streaming: before it waits at a phase boundary, every
-// wave already has the first rows of its next phase in flight.
+// share of every matrix streaming through LDS rings (global_load_lds), and a
+// workgroup that arrives at a phase boundary has the first rows of its next
+// phase in flight before it waits.  Two waves per SIMD: while one waits on
+// LDS, a shuffle or its ring, the other computes.
 //
 // Phases per layer, separated by grid barriers:
 //   QKV   input x, RMSNorm folded in; epilogue RoPE + q store + KV append
@@ -19,13 +21,13 @@
 //
 // GEMV mapping.  A phase's rows are split evenly (even counts, so RoPE pairs
 // stay together) over the workgroups.  Columns are cut into at most eight
-// slices of P block pairs (P a power of two); each wave owns one slice, its
-// lanes are (row-in-group, pair) = (lane / P, lane % P), so one load batch
-// covers 64/P rows.  A lane keeps the 64 input values of its pair in registers
-// for the whole phase, so a wave reads only P distinct 64-float blocks of the
-// LDS-staged input (stored with a per-block rotation of its 16-byte chunks so
-// those reads are bank-conflict free).  Per-row partial sums of the slices go
-// through LDS and are added in slice order.
+// slices of P block pairs (P a power of two); each wave owns a slice, its
+// lanes are (row-in-group, pair) = (lane / P, lane % P), so one item of the
+// wave's weight stream covers 64/P rows.  A lane keeps the 64 input values of
+// its pair in registers for the whole slice, so a wave reads only P distinct
+// 64-float blocks of the LDS-staged input (stored with a per-block rotation
+// of its 16-byte chunks so those reads are bank-conflict free).  Per-row
+// partial sums of the slices go through LDS and are added in slice order.
 //
 // Cross-workgroup data (activations, partials, tickets, flags, step state)
 // moves through system-scope relaxed atomics: the L2s of the eight XCDs are not
@@ -35,27 +37,24 @@
 // Grid barriers are per-workgroup epoch flags on separate cache lines, each
 // polled by one thread of every workgroup; the spin is bounded and sets an
 // error flag, after which every workgroup leaves the kernel.  A workgroup
-// raises its flag first and then issues the next phase's first loads, so the
-// wait overlaps them.
+// raises its flag first and then issues the next phase's first weight items,
+// so the wait overlaps them.
 #include "fw_device.h"
 #include "fw_kernels.h"
 #include "fw_step.h"
 
 namespace fw {
 
-constexpr int MK_WAVES = 4;                 // one wave per SIMD: 512 registers (VGPR + AGPR) each
+constexpr int MK_WAVES = 8;                 // two waves per SIMD, 256 registers each
 constexpr int MK_THREADS = MK_WAVES * 64;
 static_assert(MK_THREADS == (int)kMkThreads, "workgroup size");
-constexpr int MK_BUF = 36;                  // dwords per lane per load batch
+static_assert((int)kMkPollers <= MK_THREADS, "one barrier flag per polling thread");
+// Items per wave issued before a barrier for the phase after it.  A CU keeps
+// only some tens of KB of loads in flight: a wave issuing more stalls until
+// earlier ones land, and its own later loads (barrier polls, staged inputs)
+// complete only after its earlier ones.
+constexpr uint32_t MK_PF = 2;
 constexpr int MK_SMAX = 8;                  // column slices per row at most (64 block pairs each)
-constexpr int MK_PART = 2 * MK_SMAX;        // LDS partials per row: [matrix][slice]
-
-// Row groups per load batch: as many block pairs as fit MK_BUF dwords.
-template <uint32_t T, int M>
-__host__ __device__ constexpr int chunk_groups()
-{
-    return MK_BUF / (M * Blk<T>::pair_dw) > 0 ? MK_BUF / (M * Blk<T>::pair_dw) : 1;
-}
 
 // Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
 // what derives from it (slices, row ranges, trip counts) stays in SGPRs and
@@ -130,7 +129,7 @@ __device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *
 // staging costs one memory round trip per batch.
 __device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, const float *nw, float eps, float *s_red)
 {
-    constexpr int B = 16;
+    constexpr int B = 4096 / MK_THREADS;                 // 4096 float2 per batch
     const uint32_t n2 = n / 2;
     if (nw && n2 <= B * MK_THREADS) {                    // one batch: x and its norm weights together
         const FW_GLOBAL float2v *w2 = reinterpret_cast<const FW_GLOBAL float2v *>(gptr(nw));
@@ -193,12 +192,19 @@ __host__ __device__ inline uint32_t mk_rows_per_wg(uint32_t n_rows, uint32_t n_w
     return (per + 1) & ~1u;
 }
 
-__device__ __forceinline__ uint32_t pairs_per_slice(uint32_t n_pairs)
+__host__ __device__ inline uint32_t pairs_per_slice(uint32_t n_pairs)
 {
     const uint32_t need = (n_pairs + MK_WAVES - 1) / MK_WAVES;
     uint32_t p = 1;
     while (p < need && p < 64) p <<= 1;
     return p;
+}
+
+// Column slices of a row of n_cols values.
+__host__ __device__ inline uint32_t n_slices(uint32_t n_cols)
+{
+    const uint32_t np = n_cols / 64, p = pairs_per_slice(np);
+    return (np + p - 1) / p;
 }
 
 struct Map {
@@ -261,111 +267,248 @@ __device__ __forceinline__ const uint8_t *row_ptr(const MkGemv &g, uint32_t r, i
     }
 }
 
-// Issue the loads of this wave's row groups k0 .. k0+CH-1 (needs n_my > 0).
-// Every load is issued: a group past the wave's last one, a row past the
-// workgroup's last one and a pair past the row's end are clamped to the last
-// valid one, which the caches still hold.  Without branches around the loads
-// the compiler can count them and wait only for the batch it consumes.
-template <uint32_t T, int M>
-__device__ __forceinline__ void load_chunk(const MkGemv &g, const Map &m, uint32_t k0, uint32_t (&buf)[MK_BUF])
+// ── weight stream ────────────────────────────────────────────────────────────
+//
+// A wave's share of a phase is a sequence of items, one row group each: M
+// block pairs per lane (M = 2 for gate and up together).  Items travel from
+// HBM straight into the wave's ring of NS slots in LDS (global_load_lds: no
+// registers are held while they are in flight).  When the wave consumes an
+// item it reads the slot into registers and refills it with the item NS
+// places further on, so NS - 1 items stay in flight while it computes.
+// Vector memory loads complete in order, so the wave waits for an item with
+// s_waitcnt vmcnt((NS - 1) * D), D being the DMA instructions per item.  The
+// compiler does not track LDS written by these DMAs, so these waits are
+// explicit.  The first items of the next phase are issued right after a
+// workgroup arrives at a barrier and land during the barrier and the staging.
+//
+// A block pair is moved in 16-byte pieces and a tail (Q4_0 36 = 16+16+4,
+// Q5_0 44 = 16+16+12, Q8_0 68 = 4*16+4).  A piece of s bytes puts lane l's
+// bytes at l*s in LDS for s = 4 and 16 and at l*16 for s = 12, so a pair takes
+// 64 * (16 * n16 + 16 or 4) bytes of its slot.
+
+__host__ __device__ constexpr uint32_t dma_n16(uint32_t t) { return t == kQ8_0 ? 4u : 2u; }
+__host__ __device__ constexpr uint32_t dma_tail(uint32_t t) { return t == kQ5_0 ? 12u : 4u; }
+__host__ __device__ constexpr uint32_t dma_count(uint32_t t) { return dma_n16(t) + 1u; }
+__host__ __device__ constexpr uint32_t dma_pair_lds(uint32_t t) { return 64u * (16u * dma_n16(t) + (dma_tail(t) == 4u ? 4u : 16u)); }
+__host__ __device__ constexpr uint32_t slot_bytes(uint32_t t, uint32_t M) { return M * dma_pair_lds(t); }
+
+constexpr uint32_t MK_NS_MAX = 12;          // ring slots per wave at most
+constexpr uint32_t MK_VMCNT_MAX = 63;       // largest s_waitcnt vmcnt
+
+// Ring slots of a wave for items of type t with M matrices, given its bytes.
+__host__ __device__ inline uint32_t ring_slots(uint32_t wave_bytes, uint32_t t, uint32_t M)
 {
-    constexpr int NDW = Blk<T>::pair_dw, CH = chunk_groups<T, M>();
-    const uint32_t pair = min(m.slice * m.P + m.ps, m.n_pairs - 1);
+    uint32_t ns = wave_bytes / slot_bytes(t, M);
+    const uint32_t cap = MK_VMCNT_MAX / (dma_count(t) * M) + 1;
+    if (ns > cap) ns = cap;
+    return ns < MK_NS_MAX ? ns : MK_NS_MAX;
+}
+
+// Bytes of LDS per wave left for the ring of a phase whose input has n_in
+// values, below the fixed region at byte `fixed`.
+__host__ __device__ inline uint32_t ring_wave_bytes(uint32_t fixed, uint32_t n_in)
+{
+    const uint32_t base = (4 * n_in + 15) & ~15u;
+    return base >= fixed ? 0u : ((fixed - base) / MK_WAVES) & ~15u;
+}
+
+struct Ring {
+    uint8_t *base;            // this wave's slots
+    uint32_t ns;              // slot count
+};
+
+template <uint32_t T, int M>
+__device__ __forceinline__ Ring ring_of(uint8_t *lds, uint32_t fixed, uint32_t n_in)
+{
+    const uint32_t wb = ring_wave_bytes(fixed, n_in);
+    Ring r;
+    r.base = lds + ((4 * n_in + 15) & ~15u) + wave_id() * wb;
+    r.ns = ring_slots(wb, T, M);
+    return r;
+}
+
+// Position of an item: slice index among the wave's slices, row group in the
+// slice, ring slot.
+struct Cur {
+    uint32_t si, k, slot;
+};
+
+__device__ __forceinline__ void advance(Cur &c, uint32_t n_my, uint32_t ns)
+{
+    if (++c.k == n_my) { c.k = 0; c.si++; }
+    if (++c.slot == ns) c.slot = 0;
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <uint32_t T>
+__device__ __forceinline__ void dma_pair(const uint8_t *src, uint8_t *dst)
+{
+    const FW_GLOBAL uint8_t *s = gptr(src);
 #pragma unroll
-    for (int c = 0; c < CH; c++) {
-        const uint32_t r = min(map_row(m, min(k0 + c, m.n_my - 1)), m.hi - 1);
+    for (uint32_t i = 0; i < dma_n16(T); i++)
+        __builtin_amdgcn_global_load_lds((const FW_GLOBAL void *)(s + 16 * i), (lds_void *)(dst + 1024 * i), 16, 0, 0);
+    const FW_GLOBAL void *ts = s + 16 * dma_n16(T);
+    lds_void *td = (lds_void *)(dst + 1024 * dma_n16(T));
+    if constexpr (dma_tail(T) == 12) __builtin_amdgcn_global_load_lds(ts, td, 12, 0, 0);
+    else __builtin_amdgcn_global_load_lds(ts, td, 4, 0, 0);
+}
+
+// Issue item c.  Every load is issued: a row past the workgroup's last one and
+// a pair past the row's end are clamped to the last valid one (results of
+// such lanes are dropped), so every item counts D loads.
+template <uint32_t T, int M>
+__device__ __forceinline__ void dma_item(const MkGemv &g, const Map &m, const Cur &c, uint8_t *ring)
+{
+    const uint32_t sl = m.slice + c.si * m.sstep;
+    const uint32_t pair = min(sl * m.P + m.ps, m.n_pairs - 1);
+    const uint32_t r = min(map_row(m, c.k), m.hi - 1);
+    uint8_t *slot = ring + c.slot * slot_bytes(T, M);
 #pragma unroll
-        for (int mat = 0; mat < M; mat++)
-            load_pair<T>(row_ptr<M>(g, r, mat) + (size_t)pair * (2 * Blk<T>::bytes), buf + (c * M + mat) * NDW);
-    }
+    for (int mat = 0; mat < M; mat++)
+        dma_pair<T>(row_ptr<M>(g, r, mat) + (size_t)pair * (2 * Blk<T>::bytes), slot + mat * dma_pair_lds(T));
 }
 
 template <uint32_t T, int M>
-__device__ __forceinline__ void prefetch(const MkGemv &g, uint32_t (&buf)[MK_BUF])
+__device__ __forceinline__ void read_item(const uint8_t *slot, uint32_t (&dw)[M][Blk<T>::pair_dw])
+{
+    const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+    for (int mat = 0; mat < M; mat++) {
+        const uint8_t *p = slot + mat * dma_pair_lds(T);
+#pragma unroll
+        for (uint32_t i = 0; i < dma_n16(T); i++) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(p + 1024 * i + 16 * lane);
+            dw[mat][4 * i] = v.x; dw[mat][4 * i + 1] = v.y; dw[mat][4 * i + 2] = v.z; dw[mat][4 * i + 3] = v.w;
+        }
+        const uint8_t *t = p + 1024 * dma_n16(T);
+        if constexpr (dma_tail(T) == 4) {
+            dw[mat][4 * dma_n16(T)] = *reinterpret_cast<const uint32_t *>(t + 4 * lane);
+        } else {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(t + 16 * lane);
+            dw[mat][8] = v.x; dw[mat][9] = v.y; dw[mat][10] = v.z;
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void vmcnt_le()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until at most k items of D loads each are outstanding ((k * D) <= 63
+// for every k the ring geometry allows; larger k wait for everything).
+template <int D>
+__device__ __forceinline__ void wait_items(uint32_t k)
+{
+#define MK_W(K) case K: vmcnt_le<((K) * D <= (int)MK_VMCNT_MAX ? (K) * D : 0)>(); break;
+    switch (k) {
+    MK_W(1) MK_W(2) MK_W(3) MK_W(4) MK_W(5) MK_W(6) MK_W(7) MK_W(8) MK_W(9) MK_W(10) MK_W(11)
+    default: vmcnt_le<0>(); break;
+    }
+#undef MK_W
+}
+
+// The 64 input values of the lane's pair in slice sl (zero past the row) and,
+// for the offset formats, their two block sums.
+template <uint32_t T>
+__device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t sl, float (&xv)[64], float &sx0,
+                                       float &sx1)
+{
+    const uint32_t pair = sl * m.P + m.ps;
+    sx0 = sx1 = 0.f;
+    if (pair < m.n_pairs) {
+        const float *xp = xs + 64 * (size_t)pair;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = *reinterpret_cast<const float4 *>(xp + (((i + pair) & 15u) << 2));
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+        if constexpr (T != kQ8_0) {
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
+            sx0 = s0 + s1;
+            sx1 = s2 + s3;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 64; i++) xv[i] = 0.f;
+    }
+}
+
+// Issue the first items of g into its ring (before the barrier that precedes
+// the phase); returns how many were issued.
+template <uint32_t T, int M>
+__device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint32_t fixed)
 {
     const Map m = plan(g.n_rows, g.n_cols);
-    if (m.n_my) load_chunk<T, M>(g, m, 0, buf);
-}
-
-template <uint32_t T, int M>
-__device__ __forceinline__ void compute_chunk(const Map &m, uint32_t k0, const uint32_t (&buf)[MK_BUF],
-                                              const float (&xv)[64], float sx0, float sx1, float *part)
-{
-    constexpr int NDW = Blk<T>::pair_dw, CH = chunk_groups<T, M>();
-    const bool lane_on = m.slice * m.P + m.ps < m.n_pairs;
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-        const uint32_t k = k0 + c;
-        if (k < m.n_my) {                                    // uniform over the wave
-            const uint32_t r = map_row(m, k);
-#pragma unroll
-            for (int mat = 0; mat < M; mat++) {
-                float acc = dot_pair<T>(buf + (c * M + mat) * NDW, xv, sx0, sx1);
-                if (!lane_on || r >= m.hi) acc = 0.f;              // clamped reload
-                for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
-                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * 2 + mat) * MK_SMAX + m.slice] = acc;
-            }
-        }
+    const Ring rg = ring_of<T, M>(lds, fixed, g.n_cols);
+    const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
+    const uint32_t n = min(min(rg.ns, MK_PF), n_sl * m.n_my);
+    Cur c{0, 0, 0};
+    for (uint32_t i = 0; i < n; i++) {
+        dma_item<T, M>(g, m, c, rg.base);
+        advance(c, m.n_my, rg.ns);
     }
+    return n;
 }
 
-// This workgroup's rows of g: part[(row_local*2 + matrix)*MK_SMAX + slice].
-// A holds the first batch of the wave's first slice already when have_pre.
+// This workgroup's rows of g: part[(row_local*M + matrix)*S + slice].  The
+// first n_pre items of this wave are in flight already.
 template <uint32_t T, int M>
-__device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *part, uint32_t (&A)[MK_BUF],
-                                     bool have_pre)
+__device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *part, uint8_t *lds, uint32_t fixed,
+                                     uint32_t n_pre)
 {
-    constexpr int CH = chunk_groups<T, M>();
-    Map m = plan(g.n_rows, g.n_cols);
-    for (uint32_t sl = m.slice; sl < m.S; sl += m.sstep) {
-        const bool pre_ok = have_pre && sl == m.slice;
-        m.slice = sl;
-        const uint32_t pair = sl * m.P + m.ps;
-        float xv[64], sx0 = 0.f, sx1 = 0.f;
-        if (pair < m.n_pairs) {
-            const float *xp = xs + 64 * (size_t)pair;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float4 v = *reinterpret_cast<const float4 *>(xp + (((i + pair) & 15u) << 2));
-                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
-            }
-            if constexpr (T != kQ8_0) {
-                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-                for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
-                sx0 = s0 + s1;
-                sx1 = s2 + s3;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 64; i++) xv[i] = 0.f;
+    constexpr int D = (int)dma_count(T) * M, NDW = Blk<T>::pair_dw;
+    const Map m = plan(g.n_rows, g.n_cols);
+    const Ring rg = ring_of<T, M>(lds, fixed, g.n_cols);
+    const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
+    const uint32_t n_items = n_sl * m.n_my;
+    Cur is{0, 0, 0};
+    for (uint32_t i = 0; i < n_pre; i++) advance(is, m.n_my, rg.ns);
+    for (uint32_t i = n_pre; i < min(rg.ns, n_items); i++) {
+        dma_item<T, M>(g, m, is, rg.base);
+        advance(is, m.n_my, rg.ns);
+    }
+    Cur c{0, 0, 0};
+    float xv[64], sx0 = 0.f, sx1 = 0.f;
+    uint32_t x_si = ~0u;
+    for (uint32_t it = 0; it < n_items; it++) {
+        const uint32_t sl = m.slice + c.si * m.sstep;
+        if (c.si != x_si) {
+            x_si = c.si;
+            load_x<T>(xs, m, sl, xv, sx0, sx1);
         }
-        if (m.n_my) {
-            if (!pre_ok) load_chunk<T, M>(g, m, 0, A);
-            uint32_t B[MK_BUF];
-            const uint32_t n_chunks = (m.n_my + CH - 1) / CH;
-            for (uint32_t ch = 0; ch < n_chunks; ch += 2) {          // two named buffers, no copies
-                load_chunk<T, M>(g, m, (ch + 1) * CH, B);
-                compute_chunk<T, M>(m, ch * CH, A, xv, sx0, sx1, part);
-                load_chunk<T, M>(g, m, (ch + 2) * CH, A);
-                compute_chunk<T, M>(m, (ch + 1) * CH, B, xv, sx0, sx1, part);
-            }
+        wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
+        uint32_t dw[M][NDW];
+        read_item<T, M>(rg.base + c.slot * slot_bytes(T, M), dw);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");          // the slot is free again
+        if (it + rg.ns < n_items) {
+            dma_item<T, M>(g, m, is, rg.base);
+            advance(is, m.n_my, rg.ns);
         }
+        const uint32_t r = map_row(m, c.k);
+        const bool on = sl * m.P + m.ps < m.n_pairs && r < m.hi;
+#pragma unroll
+        for (int mat = 0; mat < M; mat++) {
+            float acc = dot_pair<T>(dw[mat], xv, sx0, sx1);
+            if (!on) acc = 0.f;
+            for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            if (m.ps == 0 && r < m.hi) part[((r - m.lo) * M + mat) * m.S + sl] = acc;
+        }
+        advance(c, m.n_my, rg.ns);
     }
     __syncthreads();
 }
 
+template <int M>
 __device__ __forceinline__ float row_sum(const float *part, uint32_t rl, int mat, uint32_t n_slices)
 {
     float y = 0.f;
-    for (uint32_t s = 0; s < n_slices; s++) y += part[(rl * 2 + mat) * MK_SMAX + s];
+    for (uint32_t s = 0; s < n_slices; s++) y += part[(rl * M + mat) * n_slices + s];
     return y;
-}
-
-__device__ __forceinline__ uint32_t n_slices_of(const MkGemv &g)
-{
-    const uint32_t np = g.n_cols / 64, p = pairs_per_slice(np);
-    return (np + p - 1) / p;
 }
 
 __device__ __forceinline__ void wg_rows(uint32_t n_rows, uint32_t &lo, uint32_t &hi)
@@ -384,11 +527,11 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices_of(g), hd = a.head_dim, half = hd / 2;
+    const uint32_t ns = n_slices(g.n_cols), hd = a.head_dim, half = hd / 2;
     const uint32_t kvd = a.n_kv * hd, nq = g.rows[0];
     for (uint32_t rl = 2 * threadIdx.x; rl < hi - lo; rl += 2 * MK_THREADS) {
         const uint32_t r = lo + rl;
-        float v0 = row_sum(part, rl, 0, ns), v1 = row_sum(part, rl + 1, 0, ns);
+        float v0 = row_sum<1>(part, rl, 0, ns), v1 = row_sum<1>(part, rl + 1, 0, ns);
         if (r < nq + kvd) {
             const uint32_t i = ((r < nq ? r : r - nq) % hd) / 2;
             const float c = rope[i], s = rope[half + i];
@@ -413,10 +556,10 @@ __device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, cons
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices_of(g);
+    const uint32_t ns = n_slices(g.n_cols);
     for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
         const uint32_t r = lo + rl;
-        const float v = x_own[rl] + row_sum(part, rl, 0, ns);
+        const float v = x_own[rl] + row_sum<1>(part, rl, 0, ns);
         x_own[rl] = v;
         st_sys(a.x + r, v);
         st_sys(trace_row + r, v);
@@ -438,9 +581,9 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices_of(g);
+    const uint32_t ns = n_slices(g.n_cols);
     for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS)
-        st_sys(a.h + lo + rl, silu_f(row_sum(part, rl, 0, ns)) * row_sum(part, rl, 1, ns));
+        st_sys(a.h + lo + rl, silu_f(row_sum<2>(part, rl, 0, ns)) * row_sum<2>(part, rl, 1, ns));
 }
 
 __device__ __forceinline__ bool am_better_mk(float v1, uint32_t i1, float v2, uint32_t i2)
@@ -480,11 +623,11 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
     __shared__ uint32_t s_last;
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices_of(g);
+    const uint32_t ns = n_slices(g.n_cols);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
-        const float y = row_sum(part, rl, 0, ns);
+        const float y = row_sum<1>(part, rl, 0, ns);
         st_sys(a.logits + lo + rl, y);
         if (!isnan(y) && (bi == 0xffffffffu || y > bv)) { bv = y; bi = lo + rl; }
     }
@@ -729,31 +872,41 @@ __device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint3
 
 // ── the kernel ───────────────────────────────────────────────────────────────
 
-// LDS layout of one workgroup, in floats (host and device agree on it).
+// LDS of one workgroup (host and device agree on it).  Below byte `fixed`: the
+// staged input of the current phase (floats from 0) and above it the waves'
+// weight rings, so a phase with a short input has deep rings.  From `fixed`
+// on, in floats: GEMV partials (or attention scratch), the layer table, this
+// workgroup's rows of x, the RoPE factors of the current position.
+constexpr uint32_t MK_LDS_BYTES = 159 * 1024;   // the static __shared__ variables take some of the rest
+
 struct MkLds {
-    uint32_t part;            // GEMV per-row slice partials (after the staged input xs at 0)
-    uint32_t tab;             // the layer table (MkLayer[n_layer])
-    uint32_t x_own;           // this workgroup's rows of x
-    uint32_t rope;            // cos (head_dim/2) then sin (head_dim/2) of the current position
-    uint32_t total;
+    uint32_t fixed;                             // bytes
+    uint32_t part, tab, x_own, rope, total;     // floats
 };
+
+__host__ __device__ inline uint32_t mk_fixed_floats(const MkArgs &a, uint32_t n_wg, uint32_t &part)
+{
+    const uint32_t kvd = a.n_kv * a.head_dim, G = a.n_head / a.n_kv;
+    part = mk_rows_per_wg(a.n_vocab, n_wg) * n_slices(a.n_embd);                       // lm-head
+    const uint32_t c[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg) * n_slices(a.n_embd),   // QKV
+                           mk_rows_per_wg(a.n_ff, n_wg) * 2 * n_slices(a.n_embd),           // gate, up
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_embd),             // WO
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff),               // down
+                           MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G,                    // attention item
+                           2 * G * a.n_splits + G };                                        // attention combine
+    for (uint32_t v : c) part = v > part ? v : part;
+    part = (part + 3) & ~3u;
+    return part + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4) + mk_rows_per_wg(a.n_embd, n_wg) + a.head_dim;
+}
 
 __host__ __device__ inline MkLds mk_layout(const MkArgs &a, uint32_t n_wg)
 {
-    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff, kvd = a.n_kv * a.head_dim;
-    uint32_t rows = mk_rows_per_wg(a.n_vocab, n_wg);
-    const uint32_t others[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg), mk_rows_per_wg(a.n_ff, n_wg),
-                                mk_rows_per_wg(a.n_embd, n_wg) };
-    for (uint32_t r : others) rows = r > rows ? r : rows;
-    const uint32_t G = a.n_head / a.n_kv;
+    uint32_t part;
+    const uint32_t nf = mk_fixed_floats(a, n_wg, part);
     MkLds L;
-    L.part = (n_max + 3) & ~3u;
-    uint32_t region = L.part + rows * MK_PART;                               // GEMV phases
-    const uint32_t item = MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G;      // attention item
-    const uint32_t comb = 2 * G * a.n_splits + G;                           // attention combine
-    region = region > item ? region : item;
-    region = region > comb ? region : comb;
-    L.tab = (region + 3) & ~3u;
+    L.fixed = (MK_LDS_BYTES - 4 * nf) & ~15u;
+    L.part = L.fixed / 4;
+    L.tab = L.part + part;
     L.x_own = L.tab + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4);
     L.rope = L.x_own + mk_rows_per_wg(a.n_embd, n_wg);
     L.total = L.rope + a.head_dim;
@@ -843,6 +996,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     __shared__ float s_red[MK_WAVES];
     __shared__ uint32_t s_fail;
     const MkLds lay = mk_layout(a, gridDim.x);
+    uint8_t *lds8 = reinterpret_cast<uint8_t *>(lds);
     float *xs = lds, *part = lds + lay.part, *x_own = lds + lay.x_own, *rope = lds + lay.rope;
     MkLayer *tab = reinterpret_cast<MkLayer *>(lds + lay.tab);
     {
@@ -852,12 +1006,10 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     }
     const uint32_t n_ops = 5 * a.n_layer + 1, half = a.head_dim / 2;
     uint32_t epoch = a.epoch0;
-    uint32_t pre[MK_BUF];
-    bool have_pre = false;
+    uint32_t n_pre = 0;                       // items of this wave's next matrix phase in flight
     const bool stamp = a.prof && blockIdx.x == 0 && threadIdx.x == 0;
     if (stamp) a.prof[0] = wall_clock64();
     __syncthreads();
-
     for (uint32_t step = 0; step < a.n_steps; step++) {
         const uint32_t tok = ld_sys(&a.state->token), pos = ld_sys(&a.state->pos);
         const uint32_t greedy = ld_sys(&a.state->greedy), n_prompt = ld_sys(&a.state->n_prompt);
@@ -870,7 +1022,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
         for (uint32_t i = 0; i < n_ops; i++) {
             const uint32_t kind = phase_kind(a, i), layer = i / 5;
             if (kind == MK_ATTN) {
-                attention(a, layer, pos, lds);
+                attention(a, layer, pos, part);
             } else if (kind == MK_HEAD && skip_head) {
                 if (blockIdx.x == 0 && threadIdx.x == 0) {
                     st_sys(&a.state->token, a.prompt[pos + 1]);
@@ -886,27 +1038,29 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 if (kind == MK_QKV && layer == 0) embed(a, xs, x_own, tok, nw, s_red);
                 else stage(xs, src, n_in, nw, a.eps, s_red);
                 const MkGemv g = phase_gemv(a, tab, kind, layer);
-                if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, pre, have_pre);
-                else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, pre, have_pre);
-                else gemv<TL, 1>(g, xs, part, pre, have_pre);
+                if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, lds8, lay.fixed, n_pre);
+                else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, n_pre);
+                else gemv<TL, 1>(g, xs, part, lds8, lay.fixed, n_pre);
                 if (kind == MK_QKV) epi_qkv(a, g, part, rope, layer, pos);
                 else if (kind == MK_FFN) epi_swiglu(a, g, part);
                 else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
                 else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd);
+                n_pre = 0;
             }
             bar_arrive(a, epoch + 1, &s_fail);
-            // first load batch of the next matrix phase, in flight across the barrier
-            // (none before attention: its registers are needed there)
-            have_pre = false;
-            const bool wrap = i + 1 == n_ops;
-            if (!wrap || step + 1 < a.n_steps) {
-                const uint32_t ni = wrap ? 0 : i + 1, nk = phase_kind(a, ni);
-                if (nk != MK_ATTN && !(nk == MK_HEAD && skip_head)) {
-                    const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
-                    if (nk == MK_FFN) prefetch<TL, 2>(ng, pre);
-                    else if (nk == MK_HEAD) prefetch<TH, 1>(ng, pre);
-                    else prefetch<TL, 1>(ng, pre);
-                    have_pre = true;
+            // the first items of the next matrix phase (past attention), in flight across the barrier
+            if (kind != MK_ATTN) {
+                const bool wrap = i + 1 == n_ops;
+                if (!wrap || step + 1 < a.n_steps) {
+                    uint32_t ni = wrap ? 0 : i + 1;
+                    if (phase_kind(a, ni) == MK_ATTN) ni++;
+                    const uint32_t nk = phase_kind(a, ni);
+                    if (!(nk == MK_HEAD && skip_head)) {
+                        const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
+                        if (nk == MK_FFN) n_pre = prefetch<TL, 2>(ng, lds8, lay.fixed);
+                        else if (nk == MK_HEAD) n_pre = prefetch<TH, 1>(ng, lds8, lay.fixed);
+                        else n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed);
+                    }
                 }
             }
             if (!bar_wait(a, ++epoch, &s_fail)) return;
@@ -928,7 +1082,19 @@ bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t gr
     return mk_type_ok(linear_type) && mk_type_ok(head_type) && (mk_type_ok(embd_type) || embd_type == kF32);
 }
 
-size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg) { return (size_t)mk_layout(a, n_wg).total * 4; }
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type)
+{
+    uint32_t part;
+    if ((size_t)4 * mk_fixed_floats(a, n_wg, part) + 16 > MK_LDS_BYTES) return 0;
+    const MkLds L = mk_layout(a, n_wg);
+    const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff;
+    if (4 * n_max > L.fixed) return 0;                               // staging
+    const uint32_t re = ring_wave_bytes(L.fixed, a.n_embd), rf = ring_wave_bytes(L.fixed, a.n_ff);
+    if (ring_slots(re, linear_type, 1) < 2 || ring_slots(re, linear_type, 2) < 2 ||
+        ring_slots(rf, linear_type, 1) < 2 || ring_slots(re, head_type, 1) < 2)
+        return 0;                                                    // rings of every phase two slots deep
+    return MK_LDS_BYTES;
+}
 
 typedef void (*mk_kernel_t)(MkArgs);
 
