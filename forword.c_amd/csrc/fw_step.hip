@@ -472,33 +472,32 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
         dma_item<T, M>(g, m, is, rg.base);
         advance(is, m.n_my, rg.ns);
     }
-    Cur c{0, 0, 0};
-    float xv[64], sx0 = 0.f, sx1 = 0.f;
-    uint32_t x_si = ~0u;
-    for (uint32_t it = 0; it < n_items; it++) {
-        const uint32_t sl = m.slice + c.si * m.sstep;
-        if (c.si != x_si) {
-            x_si = c.si;
-            load_x<T>(xs, m, sl, xv, sx0, sx1);
-        }
-        wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
-        uint32_t dw[M][NDW];
-        read_item<T, M>(rg.base + c.slot * slot_bytes(T, M), dw);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");          // the slot is free again
-        if (it + rg.ns < n_items) {
-            dma_item<T, M>(g, m, is, rg.base);
-            advance(is, m.n_my, rg.ns);
-        }
-        const uint32_t r = map_row(m, c.k);
-        const bool on = sl * m.P + m.ps < m.n_pairs && r < m.hi;
+    uint32_t it = 0, slot = 0;
+    for (uint32_t si = 0; si < n_sl; si++) {
+        const uint32_t sl = m.slice + si * m.sstep;
+        float xv[64], sx0, sx1;
+        load_x<T>(xs, m, sl, xv, sx0, sx1);
+        const bool pair_on = sl * m.P + m.ps < m.n_pairs;
+        for (uint32_t k = 0; k < m.n_my; k++, it++) {
+            wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
+            uint32_t dw[M][NDW];
+            read_item<T, M>(rg.base + slot * slot_bytes(T, M), dw);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the slot is free again
+            if (it + rg.ns < n_items) {
+                dma_item<T, M>(g, m, is, rg.base);
+                advance(is, m.n_my, rg.ns);
+            }
+            if (++slot == rg.ns) slot = 0;
+            const uint32_t r = map_row(m, k);
+            const bool on = pair_on && r < m.hi;
 #pragma unroll
-        for (int mat = 0; mat < M; mat++) {
-            float acc = dot_pair<T>(dw[mat], xv, sx0, sx1);
-            if (!on) acc = 0.f;
-            for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
-            if (m.ps == 0 && r < m.hi) part[((r - m.lo) * M + mat) * m.S + sl] = acc;
+            for (int mat = 0; mat < M; mat++) {
+                float acc = dot_pair<T>(dw[mat], xv, sx0, sx1);
+                if (!on) acc = 0.f;
+                for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
+                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * M + mat) * m.S + sl] = acc;
+            }
         }
-        advance(c, m.n_my, rg.ns);
     }
     __syncthreads();
 }
