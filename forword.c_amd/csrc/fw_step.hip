@@ -304,11 +304,18 @@ __host__ __device__ inline uint32_t ring_slots(uint32_t wave_bytes, uint32_t t, 
     return ns < MK_NS_MAX ? ns : MK_NS_MAX;
 }
 
-// Bytes of LDS per wave left for the ring of a phase whose input has n_in
-// values, below the fixed region at byte `fixed`.
-__host__ __device__ inline uint32_t ring_wave_bytes(uint32_t fixed, uint32_t n_in)
+// First byte of the rings of a phase whose input has n_in values: above the
+// staged input and above the attention scratch (the rings of the phase after
+// attention fill while it runs).
+__host__ __device__ inline uint32_t ring_base(uint32_t n_in, uint32_t attn_bytes)
 {
-    const uint32_t base = (4 * n_in + 15) & ~15u;
+    const uint32_t b = (4 * n_in + 15) & ~15u;
+    return b > attn_bytes ? b : attn_bytes;
+}
+
+// Bytes of LDS per wave for the rings between `base` and the fixed region.
+__host__ __device__ inline uint32_t ring_wave_bytes(uint32_t fixed, uint32_t base)
+{
     return base >= fixed ? 0u : ((fixed - base) / MK_WAVES) & ~15u;
 }
 
@@ -318,11 +325,11 @@ struct Ring {
 };
 
 template <uint32_t T, int M>
-__device__ __forceinline__ Ring ring_of(uint8_t *lds, uint32_t fixed, uint32_t n_in)
+__device__ __forceinline__ Ring ring_of(uint8_t *lds, uint32_t fixed, uint32_t attn_bytes, uint32_t n_in)
 {
-    const uint32_t wb = ring_wave_bytes(fixed, n_in);
+    const uint32_t base = ring_base(n_in, attn_bytes), wb = ring_wave_bytes(fixed, base);
     Ring r;
-    r.base = lds + ((4 * n_in + 15) & ~15u) + wave_id() * wb;
+    r.base = lds + base + wave_id() * wb;
     r.ns = ring_slots(wb, T, M);
     return r;
 }
@@ -441,10 +448,10 @@ __device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t s
 // Issue the first items of g into its ring (before the barrier that precedes
 // the phase); returns how many were issued.
 template <uint32_t T, int M>
-__device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint32_t fixed)
+__device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint32_t fixed, uint32_t attn_bytes)
 {
     const Map m = plan(g.n_rows, g.n_cols);
-    const Ring rg = ring_of<T, M>(lds, fixed, g.n_cols);
+    const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
     const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
     const uint32_t n = min(min(rg.ns, MK_PF), n_sl * m.n_my);
     Cur c{0, 0, 0};
@@ -459,11 +466,11 @@ __device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint
 // first n_pre items of this wave are in flight already.
 template <uint32_t T, int M>
 __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *part, uint8_t *lds, uint32_t fixed,
-                                     uint32_t n_pre)
+                                     uint32_t attn_bytes, uint32_t n_pre)
 {
     constexpr int D = (int)dma_count(T) * M, NDW = Blk<T>::pair_dw;
     const Map m = plan(g.n_rows, g.n_cols);
-    const Ring rg = ring_of<T, M>(lds, fixed, g.n_cols);
+    const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
     const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
     const uint32_t n_items = n_sl * m.n_my;
     Cur is{0, 0, 0};
@@ -872,30 +879,37 @@ __device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint3
 // ── the kernel ───────────────────────────────────────────────────────────────
 
 // LDS of one workgroup (host and device agree on it).  Below byte `fixed`: the
-// staged input of the current phase (floats from 0) and above it the waves'
-// weight rings, so a phase with a short input has deep rings.  From `fixed`
+// staged input of the current phase (floats from 0) or the attention scratch,
+// and above them the waves' weight rings, so a phase with a short input has
+// deep rings.  From `fixed`
 // on, in floats: GEMV partials (or attention scratch), the layer table, this
 // workgroup's rows of x, the RoPE factors of the current position.
 constexpr uint32_t MK_LDS_BYTES = 159 * 1024;   // the static __shared__ variables take some of the rest
 
 struct MkLds {
-    uint32_t fixed;                             // bytes
+    uint32_t fixed, attn;                       // bytes: fixed region, attention scratch (from 0)
     uint32_t part, tab, x_own, rope, total;     // floats
 };
 
 __host__ __device__ inline uint32_t mk_fixed_floats(const MkArgs &a, uint32_t n_wg, uint32_t &part)
 {
-    const uint32_t kvd = a.n_kv * a.head_dim, G = a.n_head / a.n_kv;
+    const uint32_t kvd = a.n_kv * a.head_dim;
     part = mk_rows_per_wg(a.n_vocab, n_wg) * n_slices(a.n_embd);                       // lm-head
     const uint32_t c[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg) * n_slices(a.n_embd),   // QKV
                            mk_rows_per_wg(a.n_ff, n_wg) * 2 * n_slices(a.n_embd),           // gate, up
                            mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_embd),             // WO
-                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff),               // down
-                           MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G,                    // attention item
-                           2 * G * a.n_splits + G };                                        // attention combine
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff) };             // down
     for (uint32_t v : c) part = v > part ? v : part;
     part = (part + 3) & ~3u;
     return part + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4) + mk_rows_per_wg(a.n_embd, n_wg) + a.head_dim;
+}
+
+// Attention scratch (an item's per-wave partials, then the combine), from byte 0.
+__host__ __device__ inline uint32_t mk_attn_bytes(const MkArgs &a)
+{
+    const uint32_t G = a.n_head / a.n_kv;
+    const uint32_t item = MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G, comb = 2 * G * a.n_splits + G;
+    return ((item > comb ? item : comb) * 4 + 15) & ~15u;
 }
 
 __host__ __device__ inline MkLds mk_layout(const MkArgs &a, uint32_t n_wg)
@@ -904,6 +918,7 @@ __host__ __device__ inline MkLds mk_layout(const MkArgs &a, uint32_t n_wg)
     const uint32_t nf = mk_fixed_floats(a, n_wg, part);
     MkLds L;
     L.fixed = (MK_LDS_BYTES - 4 * nf) & ~15u;
+    L.attn = mk_attn_bytes(a);
     L.part = L.fixed / 4;
     L.tab = L.part + part;
     L.x_own = L.tab + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4);
@@ -1021,7 +1036,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
         for (uint32_t i = 0; i < n_ops; i++) {
             const uint32_t kind = phase_kind(a, i), layer = i / 5;
             if (kind == MK_ATTN) {
-                attention(a, layer, pos, part);
+                attention(a, layer, pos, lds);
             } else if (kind == MK_HEAD && skip_head) {
                 if (blockIdx.x == 0 && threadIdx.x == 0) {
                     st_sys(&a.state->token, a.prompt[pos + 1]);
@@ -1037,9 +1052,9 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 if (kind == MK_QKV && layer == 0) embed(a, xs, x_own, tok, nw, s_red);
                 else stage(xs, src, n_in, nw, a.eps, s_red);
                 const MkGemv g = phase_gemv(a, tab, kind, layer);
-                if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, lds8, lay.fixed, n_pre);
-                else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, n_pre);
-                else gemv<TL, 1>(g, xs, part, lds8, lay.fixed, n_pre);
+                if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                else gemv<TL, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 if (kind == MK_QKV) epi_qkv(a, g, part, rope, layer, pos);
                 else if (kind == MK_FFN) epi_swiglu(a, g, part);
                 else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
@@ -1056,9 +1071,9 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                     const uint32_t nk = phase_kind(a, ni);
                     if (!(nk == MK_HEAD && skip_head)) {
                         const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
-                        if (nk == MK_FFN) n_pre = prefetch<TL, 2>(ng, lds8, lay.fixed);
-                        else if (nk == MK_HEAD) n_pre = prefetch<TH, 1>(ng, lds8, lay.fixed);
-                        else n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed);
+                        if (nk == MK_FFN) n_pre = prefetch<TL, 2>(ng, lds8, lay.fixed, lay.attn);
+                        else if (nk == MK_HEAD) n_pre = prefetch<TH, 1>(ng, lds8, lay.fixed, lay.attn);
+                        else n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);
                     }
                 }
             }
@@ -1087,11 +1102,12 @@ size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32
     if ((size_t)4 * mk_fixed_floats(a, n_wg, part) + 16 > MK_LDS_BYTES) return 0;
     const MkLds L = mk_layout(a, n_wg);
     const uint32_t n_max = a.n_embd > a.n_ff ? a.n_embd : a.n_ff;
-    if (4 * n_max > L.fixed) return 0;                               // staging
-    const uint32_t re = ring_wave_bytes(L.fixed, a.n_embd), rf = ring_wave_bytes(L.fixed, a.n_ff);
-    if (ring_slots(re, linear_type, 1) < 2 || ring_slots(re, linear_type, 2) < 2 ||
-        ring_slots(rf, linear_type, 1) < 2 || ring_slots(re, head_type, 1) < 2)
-        return 0;                                                    // rings of every phase two slots deep
+    if (4 * n_max > L.fixed || L.attn > L.fixed) return 0;           // staging, attention scratch
+    const uint32_t re = ring_wave_bytes(L.fixed, ring_base(a.n_embd, L.attn));
+    const uint32_t rf = ring_wave_bytes(L.fixed, ring_base(a.n_ff, L.attn));
+    if (ring_slots(re, linear_type, 1) < 1 || ring_slots(re, linear_type, 2) < 1 ||
+        ring_slots(rf, linear_type, 1) < 1 || ring_slots(re, head_type, 1) < 1)
+        return 0;                                                    // a ring slot for every phase
     return MK_LDS_BYTES;
 }
 
