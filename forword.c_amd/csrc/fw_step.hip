@@ -56,10 +56,21 @@ static_assert((int)kMkPollers <= MK_THREADS, "one barrier flag per polling threa
 constexpr uint32_t MK_PF = 2;
 constexpr int MK_SMAX = 8;                  // column slices per row at most (64 block pairs each)
 
+// threadIdx.x through an opaque move.  Values derived from it are then formed
+// where each phase uses them; otherwise the compiler hoists every phase's
+// per-lane values out of the step loop and keeps them all live across every
+// phase (256 registers and spills instead of under 200).
+__device__ __forceinline__ uint32_t tid()
+{
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // Index of the calling wave in its workgroup, as a wave-uniform (scalar) value:
 // what derives from it (slices, row ranges, trip counts) stays in SGPRs and
 // the loops over it branch uniformly.
-__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(tid() >> 6); }
 
 // Position of input element j in the LDS staging area.
 __device__ __forceinline__ uint32_t swz(uint32_t j)
@@ -74,9 +85,9 @@ __device__ __forceinline__ uint32_t swz(uint32_t j)
 __device__ __forceinline__ void bar_arrive(const MkArgs &a, uint32_t epoch, uint32_t *s_fail)
 {
     wait_mem();
-    if (threadIdx.x == 0) *s_fail = 0;
+    if (tid() == 0) *s_fail = 0;
     __syncthreads();
-    if (threadIdx.x == 0) st_sys(a.bar + blockIdx.x * 32, epoch);
+    if (tid() == 0) st_sys(a.bar + blockIdx.x * 32, epoch);
 }
 
 // Wait until every workgroup's flag has reached epoch: thread t polls the flag
@@ -84,9 +95,9 @@ __device__ __forceinline__ void bar_arrive(const MkArgs &a, uint32_t epoch, uint
 // error word; the caller then leaves the kernel.
 __device__ __forceinline__ bool bar_wait(const MkArgs &a, uint32_t epoch, uint32_t *s_fail)
 {
-    if (threadIdx.x < gridDim.x) {
+    if (tid() < gridDim.x) {
         uint32_t spins = 0;
-        while ((int)(ld_sys(a.bar + threadIdx.x * 32) - epoch) < 0) {
+        while ((int)(ld_sys(a.bar + tid() * 32) - epoch) < 0) {
             if (++spins > (1u << 22) || ld_sys(a.err) != 0) {
                 atomicOr(a.err, 1u);
                 *s_fail = 1;
@@ -103,7 +114,7 @@ __device__ __forceinline__ bool bar_wait(const MkArgs &a, uint32_t epoch, uint32
 __device__ __forceinline__ float block_sum_all(float v, float *s_red)
 {
     v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int lane = tid() & 63, wave = wave_id();
     __syncthreads();
     if (lane == 0) s_red[wave] = v;
     __syncthreads();
@@ -120,7 +131,7 @@ __device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *
     ss = block_sum_all(ss, s_red);                       // also orders every thread's staging stores
     const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
     const FW_GLOBAL float *w = gptr(nw);
-    for (uint32_t j = threadIdx.x; j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * w[j]) * scale;
+    for (uint32_t j = tid(); j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * w[j]) * scale;
 }
 
 // xs <- src (n floats, n even, optionally RMS-normalised by weights nw), src
@@ -136,13 +147,13 @@ __device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, c
         float2v v[B], w[B];
 #pragma unroll
         for (int b = 0; b < B; b++) {
-            const uint32_t j = threadIdx.x + b * MK_THREADS;
+            const uint32_t j = tid() + b * MK_THREADS;
             if (j < n2) { v[b] = ld_sys2(src + 2 * j); w[b] = w2[j]; }
         }
         float ss = 0.f;
 #pragma unroll
         for (int b = 0; b < B; b++)
-            if (threadIdx.x + b * MK_THREADS < n2) {
+            if (tid() + b * MK_THREADS < n2) {
                 ss = __builtin_fmaf(v[b][0], v[b][0], ss);
                 ss = __builtin_fmaf(v[b][1], v[b][1], ss);
             }
@@ -150,7 +161,7 @@ __device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, c
         const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
 #pragma unroll
         for (int b = 0; b < B; b++) {
-            const uint32_t j = threadIdx.x + b * MK_THREADS;
+            const uint32_t j = tid() + b * MK_THREADS;
             if (j < n2) {
                 float2v o;
                 o[0] = (v[b][0] * w[b][0]) * scale;
@@ -162,7 +173,7 @@ __device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, c
         return;
     }
     float ss = 0.f;
-    for (uint32_t j0 = threadIdx.x; j0 < n2; j0 += 2 * B * MK_THREADS) {
+    for (uint32_t j0 = tid(); j0 < n2; j0 += 2 * B * MK_THREADS) {
         float2v v[2 * B];
 #pragma unroll
         for (int b = 0; b < 2 * B; b++) {
@@ -227,7 +238,7 @@ __device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols)
     m.n_pairs = n_cols / 64;
     m.P = pairs_per_slice(m.n_pairs);
     m.S = (m.n_pairs + m.P - 1) / m.P;
-    const uint32_t wave = wave_id(), lane = threadIdx.x & 63;
+    const uint32_t wave = wave_id(), lane = tid() & 63;
     if (m.S <= (uint32_t)MK_WAVES) {
         m.slice = wave % m.S;
         m.sstep = MK_SMAX;
@@ -379,7 +390,7 @@ __device__ __forceinline__ void dma_item(const MkGemv &g, const Map &m, const Cu
 template <uint32_t T, int M>
 __device__ __forceinline__ void read_item(const uint8_t *slot, uint32_t (&dw)[M][Blk<T>::pair_dw])
 {
-    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t lane = tid() & 63;
 #pragma unroll
     for (int mat = 0; mat < M; mat++) {
         const uint8_t *p = slot + mat * dma_pair_lds(T);
@@ -535,7 +546,7 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices(g.n_cols), hd = a.head_dim, half = hd / 2;
     const uint32_t kvd = a.n_kv * hd, nq = g.rows[0];
-    for (uint32_t rl = 2 * threadIdx.x; rl < hi - lo; rl += 2 * MK_THREADS) {
+    for (uint32_t rl = 2 * tid(); rl < hi - lo; rl += 2 * MK_THREADS) {
         const uint32_t r = lo + rl;
         float v0 = row_sum<1>(part, rl, 0, ns), v1 = row_sum<1>(part, rl + 1, 0, ns);
         if (r < nq + kvd) {
@@ -563,7 +574,7 @@ __device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, cons
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices(g.n_cols);
-    for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
+    for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const uint32_t r = lo + rl;
         const float v = x_own[rl] + row_sum<1>(part, rl, 0, ns);
         x_own[rl] = v;
@@ -588,7 +599,7 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices(g.n_cols);
-    for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS)
+    for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS)
         st_sys(a.h + lo + rl, silu_f(row_sum<2>(part, rl, 0, ns)) * row_sum<2>(part, rl, 1, ns));
 }
 
@@ -608,11 +619,11 @@ __device__ __forceinline__ void block_best(float &bv, uint32_t &bi, float *s_v, 
         const uint32_t oi = __shfl_xor(bi, m, 64);
         if (am_better_mk(ov, oi, bv, bi)) { bv = ov; bi = oi; }
     }
-    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int lane = tid() & 63, wave = wave_id();
     __syncthreads();
     if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0)
+    if (tid() == 0)
         for (int w = 1; w < MK_WAVES; w++)
             if (am_better_mk(s_v[w], s_i[w], bv, bi)) { bv = s_v[w]; bi = s_i[w]; }
 }
@@ -632,14 +643,14 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
     const uint32_t ns = n_slices(g.n_cols);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
-    for (uint32_t rl = threadIdx.x; rl < hi - lo; rl += MK_THREADS) {
+    for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const float y = row_sum<1>(part, rl, 0, ns);
         st_sys(a.logits + lo + rl, y);
         if (!isnan(y) && (bi == 0xffffffffu || y > bv)) { bv = y; bi = lo + rl; }
     }
     wait_mem();
     block_best(bv, bi, s_v, s_i);
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
         st_sys(a.am_v + blockIdx.x, bv);
         st_sys(a.am_i + blockIdx.x, bi);
         wait_mem();
@@ -649,13 +660,13 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
     if (!s_last) return;
     bv = -INFINITY;
     bi = 0xffffffffu;
-    for (uint32_t w = threadIdx.x; w < gridDim.x; w += MK_THREADS) {
+    for (uint32_t w = tid(); w < gridDim.x; w += MK_THREADS) {
         const float v = ld_sys(a.am_v + w);
         const uint32_t i = ld_sys(a.am_i + w);
         if (am_better_mk(v, i, bv, bi)) { bv = v; bi = i; }
     }
     block_best(bv, bi, s_v, s_i);
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
         const uint32_t r = (bi == 0xffffffffu || isnan(ld_sys(a.logits))) ? 0u : bi;
         st_sys(a.argmax_out, r);
         st_sys(&a.state->next, r);
@@ -684,6 +695,64 @@ __device__ __forceinline__ void load_vec(const FW_GLOBAL float *p, float (&v)[EP
     }
 }
 
+// Positions t = first, first + NG, ... below t1 (NG = 2 * MK_WAVES) into the
+// running (m, l, o) of the G heads: a batch of U positions is loaded at once
+// (positions past t1 reload the batch's first one and get no weight), all
+// U * G scores are formed, then each head is rescaled once per batch.
+template <int EPL, int G, int U>
+__device__ __forceinline__ void attn_batches(const FW_GLOBAL float *kc, const FW_GLOBAL float *vc, size_t kvd,
+                                             const float (&qv)[G][EPL], float sc, uint32_t first, uint32_t t1,
+                                             float (&m)[G], float (&l)[G], float (&o)[G][EPL])
+{
+    constexpr uint32_t NG = 2 * MK_WAVES;
+    for (uint32_t tb = first; tb < t1; tb += U * NG) {
+        float kk[U][EPL], vv[U][EPL];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t t = tb + u * NG < t1 ? tb + u * NG : tb;
+            load_vec<EPL>(kc + (size_t)t * kvd, kk[u]);
+            load_vec<EPL>(vc + (size_t)t * kvd, vv[u]);
+        }
+        float s[U][G];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[u][e], d);
+                s[u][g] = d;
+            }
+#pragma unroll
+        for (int o2 = 16; o2 >= 1; o2 >>= 1)
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int g = 0; g < G; g++) s[u][g] += __shfl_xor(s[u][g], o2, 64);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float mx = m[g];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                s[u][g] = tb + u * NG < t1 ? s[u][g] * sc : -INFINITY;
+                mx = fmaxf(mx, s[u][g]);                     // finite: position tb is below t1
+            }
+            const float c = exp2f(m[g] - mx);
+            l[g] *= c;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[g][e] *= c;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const float pe = exp2f(s[u][g] - mx);
+                l[g] += pe;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(pe, vv[u][e], o[g][e]);
+            }
+            m[g] = mx;
+        }
+    }
+}
+
 // One (KV head, split) item: online softmax (log2 domain) over the split's
 // positions for the G query heads of the group (attention.c:142-164); partial
 // (o[HD], m, l) per query head to a.part.  A position is spread over 32 lanes
@@ -697,7 +766,7 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
     float (*s_l)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD + MK_WAVES * G);
     const uint32_t n_pos = pos + 1, ns = a.n_splits, chunk = (n_pos + ns - 1) / ns;
     const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
-    const int lane = threadIdx.x & 63, wave = wave_id(), grp = lane >> 5, l32 = lane & 31;
+    const int lane = tid() & 63, wave = wave_id(), grp = lane >> 5, l32 = lane & 31;
     const size_t kvd = (size_t)a.n_kv * HD;
     const FW_GLOBAL float *kc = gptr(a.kc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
     const FW_GLOBAL float *vc = gptr(a.vc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
@@ -714,35 +783,11 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
             o[g][e] = 0.f;
         }
     }
-    // two positions per lane group per iteration, both loads issued first; the
-    // second one past the split's end reloads the first and is given no weight
-    for (uint32_t t = t0 + wave * 2 + grp; t < t1; t += 4 * MK_WAVES) {
-        const bool has2 = t + 2 * MK_WAVES < t1;
-        const uint32_t t2 = has2 ? t + 2 * MK_WAVES : t;
-        float kk[2][EPL], vv[2][EPL];
-        load_vec<EPL>(kc + (size_t)t * kvd, kk[0]);
-        load_vec<EPL>(vc + (size_t)t * kvd, vv[0]);
-        load_vec<EPL>(kc + (size_t)t2 * kvd, kk[1]);
-        load_vec<EPL>(vc + (size_t)t2 * kvd, vv[1]);
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[u][e], d);
-#pragma unroll
-                for (int o2 = 16; o2 >= 1; o2 >>= 1) d += __shfl_xor(d, o2, 64);
-                const float s = (u == 0 || has2) ? d * sc : -INFINITY;     // m[g] is finite after u = 0
-                const float mn = fmaxf(m[g], s);
-                const float c = exp2f(m[g] - mn), pe = exp2f(s - mn);
-                l[g] = __builtin_fmaf(l[g], c, pe);
-#pragma unroll
-                for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(o[g][e], c, pe * vv[u][e]);
-                m[g] = mn;
-            }
-        }
-    }
+    // Each 32-lane group walks positions first, first + 2 * MK_WAVES, ...; in
+    // batches of U (more for long splits).
+    const uint32_t first = t0 + wave * 2 + grp, per_group = (t1 - t0 + 2 * MK_WAVES - 1) / (2 * MK_WAVES);
+    if (per_group <= 2) attn_batches<EPL, G, 2>(kc, vc, kvd, qv, sc, first, t1, m, l, o);
+    else attn_batches<EPL, G, EPL == 4 ? 4 : 8>(kc, vc, kvd, qv, sc, first, t1, m, l, o);
 #pragma unroll
     for (int g = 0; g < G; g++) {                          // merge the wave's two position groups
         const float mw = fmaxf(m[g], __shfl_xor(m[g], 32, 64));
@@ -768,7 +813,7 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < G * HD; i += MK_THREADS) {   // merge the eight waves
+    for (int i = tid(); i < G * HD; i += MK_THREADS) {   // merge the eight waves
         const int g = i / HD, dd = i % HD;
         float M = -INFINITY;
 #pragma unroll
@@ -799,13 +844,13 @@ __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, floa
     float *s_l = lds + G * ns;                             // [G][ns] l
     float *s_inv = lds + 2 * G * ns;                       // [G] 1 / sum of weights
     const float *base = a.part + (size_t)kvh * G * ns * (HD + 2);   // (head g, split s) at (g*ns + s)*(HD+2)
-    for (uint32_t t = threadIdx.x; t < G * ns; t += MK_THREADS) {
+    for (uint32_t t = tid(); t < G * ns; t += MK_THREADS) {
         const float2v ml = ld_sys2(base + (size_t)t * (HD + 2) + HD);
         s_w[t] = ml[0];
         s_l[t] = ml[1];
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
+    const int lane = tid() & 63;
     for (uint32_t g = wave_id(); g < (uint32_t)G; g += MK_WAVES) {
         float M = -INFINITY;
         for (uint32_t s = lane; s < ns; s += 64) M = fmaxf(M, s_w[g * ns + s]);
@@ -821,7 +866,7 @@ __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, floa
         if (lane == 0) s_inv[g] = 1.0f / L;
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < (uint32_t)(G * HD); i += MK_THREADS) {
+    for (uint32_t i = tid(); i < (uint32_t)(G * HD); i += MK_THREADS) {
         const uint32_t g = i / HD, d = i % HD;
         const float *pp = base + (size_t)g * ns * (HD + 2) + d;
         const float *w = s_w + g * ns;
@@ -847,11 +892,11 @@ __device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uin
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint32_t kvh = it % a.n_kv, split = it / a.n_kv;
         attn_item<EPL, G>(a, layer, pos, kvh, split, lds);
-        if (threadIdx.x == 0) s_last = ticket_sys(a.tickets + kvh) == a.n_splits - 1;
+        if (tid() == 0) s_last = ticket_sys(a.tickets + kvh) == a.n_splits - 1;
         __syncthreads();
         if (s_last) {
             attn_combine<EPL, G>(a, kvh, lds);
-            if (threadIdx.x == 0) st_sys(a.tickets + kvh, 0u);
+            if (tid() == 0) st_sys(a.tickets + kvh, 0u);
         }
     }
 }
@@ -983,7 +1028,7 @@ __device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, 
     const uint8_t *row = a.embd + (size_t)tok * a.embd_row_bytes;
     const uint32_t bb = block_bytes_dev(a.embd_type);
     float ss = 0.f;
-    for (uint32_t j = threadIdx.x; j < a.n_embd; j += MK_THREADS) {
+    for (uint32_t j = tid(); j < a.n_embd; j += MK_THREADS) {
         float v = a.embd_type == kF32 ? reinterpret_cast<const float *>(row)[j]
                                       : dequant_one(row + (size_t)(j / 32) * bb, a.embd_type, j & 31);
         if (a.embd_scale != 1.0f) v *= a.embd_scale;
@@ -1016,19 +1061,19 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     {
         const uint32_t *src = reinterpret_cast<const uint32_t *>(a.layers);
         uint32_t *dst = reinterpret_cast<uint32_t *>(tab);
-        for (uint32_t j = threadIdx.x; j < a.n_layer * (uint32_t)(sizeof(MkLayer) / 4); j += MK_THREADS) dst[j] = src[j];
+        for (uint32_t j = tid(); j < a.n_layer * (uint32_t)(sizeof(MkLayer) / 4); j += MK_THREADS) dst[j] = src[j];
     }
     const uint32_t n_ops = 5 * a.n_layer + 1, half = a.head_dim / 2;
     uint32_t epoch = a.epoch0;
     uint32_t n_pre = 0;                       // items of this wave's next matrix phase in flight
-    const bool stamp = a.prof && blockIdx.x == 0 && threadIdx.x == 0;
+    const bool stamp = a.prof && blockIdx.x == 0 && tid() == 0;
     if (stamp) a.prof[0] = wall_clock64();
     __syncthreads();
     for (uint32_t step = 0; step < a.n_steps; step++) {
         const uint32_t tok = ld_sys(&a.state->token), pos = ld_sys(&a.state->pos);
         const uint32_t greedy = ld_sys(&a.state->greedy), n_prompt = ld_sys(&a.state->n_prompt);
         const bool skip_head = greedy && pos + 1 < n_prompt;   // prefill: logits never read
-        for (uint32_t t = threadIdx.x; t < half; t += MK_THREADS) {
+        for (uint32_t t = tid(); t < half; t += MK_THREADS) {
             rope[t] = a.cos_tab[(size_t)pos * half + t];
             rope[half + t] = a.sin_tab[(size_t)pos * half + t];
         }
@@ -1038,7 +1083,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
             if (kind == MK_ATTN) {
                 attention(a, layer, pos, lds);
             } else if (kind == MK_HEAD && skip_head) {
-                if (blockIdx.x == 0 && threadIdx.x == 0) {
+                if (blockIdx.x == 0 && tid() == 0) {
                     st_sys(&a.state->token, a.prompt[pos + 1]);
                     st_sys(&a.state->pos, pos + 1);
                 }
