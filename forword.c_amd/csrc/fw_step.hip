@@ -473,6 +473,47 @@ __device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint
     return n;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of P lanes (P a power of two, wave-uniform); the
+// group's first lane (at least) ends with the sum.  DPP quad permutes give
+// the sums of 2 and 4 lanes; once the 4-lane groups hold equal values, adding
+// the half-row mirror (lane 7 - i) and row mirror (lane 15 - i) gives those of
+// 8 and 16; a swizzle and a permute give 32 and 64.
+template <int M>
+__device__ __forceinline__ void lane_sum(float (&v)[M], uint32_t P)
+{
+    if (P >= 2) {
+#pragma unroll
+        for (int i = 0; i < M; i++) v[i] += dpp<0xB1>(v[i]);                 // quad_perm 1,0,3,2
+    }
+    if (P >= 4) {
+#pragma unroll
+        for (int i = 0; i < M; i++) v[i] += dpp<0x4E>(v[i]);                 // quad_perm 2,3,0,1
+    }
+    if (P >= 8) {
+#pragma unroll
+        for (int i = 0; i < M; i++) v[i] += dpp<0x141>(v[i]);                // row_half_mirror
+    }
+    if (P >= 16) {
+#pragma unroll
+        for (int i = 0; i < M; i++) v[i] += dpp<0x140>(v[i]);                // row_mirror
+    }
+    if (P >= 32) {
+#pragma unroll
+        for (int i = 0; i < M; i++)                                          // lane ^ 16 (swizzle bit masks)
+            v[i] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[i]), 0x401F));
+    }
+    if (P >= 64) {
+#pragma unroll
+        for (int i = 0; i < M; i++) v[i] += __shfl_xor(v[i], 32, 64);
+    }
+}
+
 // This workgroup's rows of g: part[(row_local*M + matrix)*S + slice].  The
 // first n_pre items of this wave are in flight already.
 template <uint32_t T, int M>
@@ -508,13 +549,16 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
             if (++slot == rg.ns) slot = 0;
             const uint32_t r = map_row(m, k);
             const bool on = pair_on && r < m.hi;
+            float acc[M];
 #pragma unroll
             for (int mat = 0; mat < M; mat++) {
-                float acc = dot_pair<T>(dw[mat], xv, sx0, sx1);
-                if (!on) acc = 0.f;
-                for (uint32_t o = m.P >> 1; o; o >>= 1) acc += __shfl_xor(acc, o, 64);
-                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * M + mat) * m.S + sl] = acc;
+                acc[mat] = dot_pair<T>(dw[mat], xv, sx0, sx1);
+                if (!on) acc[mat] = 0.f;
             }
+            lane_sum<M>(acc, m.P);
+#pragma unroll
+            for (int mat = 0; mat < M; mat++)
+                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * M + mat) * m.S + sl] = acc[mat];
         }
     }
     __syncthreads();
@@ -724,11 +768,7 @@ __device__ __forceinline__ void attn_batches(const FW_GLOBAL float *kc, const FW
                 s[u][g] = d;
             }
 #pragma unroll
-        for (int o2 = 16; o2 >= 1; o2 >>= 1)
-#pragma unroll
-            for (int u = 0; u < U; u++)
-#pragma unroll
-                for (int g = 0; g < G; g++) s[u][g] += __shfl_xor(s[u][g], o2, 64);
+        for (int u = 0; u < U; u++) lane_sum<G>(s[u], 32);          // every lane of the group gets the sum
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float mx = m[g];
