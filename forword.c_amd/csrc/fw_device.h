@@ -270,6 +270,20 @@ __device__ __forceinline__ float2v ld_sys2(const float *p)
     r[1] = __builtin_bit_cast(float, (uint32_t)(v >> 32));
     return r;
 }
+// A published value with the epoch it belongs to, stored and loaded as one
+// 64-bit single-copy-atomic word: a reader that sees the tag sees the value.
+__device__ __forceinline__ uint64_t tagged(float v, uint32_t tag)
+{
+    return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)tag << 32);
+}
+__device__ __forceinline__ void st_sys64(uint64_t *p, uint64_t v)
+{
+    __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t ld_sys64(const uint64_t *p)
+{
+    return __hip_atomic_load(gptr(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 __device__ __forceinline__ uint32_t ticket_sys(uint32_t *p)
 {
     return __hip_atomic_fetch_add(gptr(p), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);

@@ -105,6 +105,7 @@ struct forword_gpu {
     MkArgs mka{};
     uint32_t *d_bar = nullptr, *d_mk_err = nullptr, *d_mk_tickets = nullptr, *d_ami = nullptr;
     float *d_amv = nullptr, *d_mk_part = nullptr;
+    uint64_t *d_tx = nullptr, *d_tatt = nullptr, *d_th = nullptr;   // tagged activations of the persistent kernel
     MkLayer *d_layers = nullptr;
     uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
     uint32_t prof_steps = 0;
@@ -327,7 +328,7 @@ static int setup_mk(forword_gpu_t *h)
     a.n_embd = n; a.n_ff = c.n_ff; a.n_head = c.n_head; a.n_kv = c.n_head_kv; a.head_dim = hd;
     a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
     a.kc = h->d_k; a.vc = h->d_v; a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
-    a.x = h->d_x; a.q = h->d_q; a.att = h->d_att; a.h = h->d_h; a.logits = h->d_logits; a.trace = h->d_trace;
+    a.q = h->d_q; a.logits = h->d_logits; a.trace = h->d_trace;
     a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
     // (KV head, split) attention items: about one per workgroup, >= 8 positions per split
     uint32_t ns = (uint32_t)cus / c.n_head_kv;
@@ -352,11 +353,17 @@ static int setup_mk(forword_gpu_t *h)
         dalloc(h, (void **)&h->d_bar, (size_t)wg * 128, "barrier flags") ||
         dalloc(h, (void **)&h->d_mk_tickets, 64 * 4, "tickets") || dalloc(h, (void **)&h->d_mk_err, 4, "barrier status") ||
         dalloc(h, (void **)&h->d_amv, (size_t)wg * 4, "argmax") || dalloc(h, (void **)&h->d_ami, (size_t)wg * 4, "argmax") ||
-        dalloc(h, (void **)&h->d_mk_part, (size_t)c.n_head * ns * (hd + 2) * 4, "attention partials"))
+        dalloc(h, (void **)&h->d_mk_part, (size_t)c.n_head * ns * (hd + 2) * 4, "attention partials") ||
+        dalloc(h, (void **)&h->d_tx, (size_t)n * 8, "tagged x") ||
+        dalloc(h, (void **)&h->d_tatt, (size_t)n * 8, "tagged attention output") ||
+        dalloc(h, (void **)&h->d_th, (size_t)c.n_ff * 8, "tagged ffn activations"))
         return -1;
+    a.tx = h->d_tx; a.tatt = h->d_tatt; a.th = h->d_th;
     if (hipMemcpy(h->d_layers, layers.data(), layers.size() * sizeof(MkLayer), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(h->d_bar, 0, (size_t)wg * 128) != hipSuccess || hipMemset(h->d_mk_tickets, 0, 64 * 4) != hipSuccess ||
-        hipMemset(h->d_mk_err, 0, 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipMemset(h->d_mk_err, 0, 4) != hipSuccess || hipMemset(h->d_tx, 0, (size_t)n * 8) != hipSuccess ||
+        hipMemset(h->d_tatt, 0, (size_t)n * 8) != hipSuccess || hipMemset(h->d_th, 0, (size_t)c.n_ff * 8) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
         set_err("persistent step kernel: device set-up failed");
         return -1;
     }

@@ -46,7 +46,10 @@ struct MkArgs {
     float eps;
     float *kc, *vc;
     const float *cos_tab, *sin_tab;
-    float *x, *q, *att, *h, *logits;
+    float *q, *logits;
+    // Activations passed between phases without a grid barrier, as {value,
+    // epoch} words (see tagged()): residual stream x, attention output, ffn h.
+    uint64_t *tx, *tatt, *th;
     float *trace;            // [2 * n_layer][n_embd] residual stream after each residual add
     float *part;             // attention partials [n_head][n_splits][head_dim + 2]
     StepState *state;
@@ -54,7 +57,7 @@ struct MkArgs {
     uint32_t *ids, *argmax_out;
     uint32_t *bar;           // one barrier flag per workgroup, 128 bytes apart
     uint32_t *tickets;       // n_kv attention-combine tickets + 1 argmax ticket, zero between uses
-    uint32_t *err;           // set when a barrier wait gives up
+    uint32_t *err;           // set when a barrier or tagged-value wait gives up
     float *am_v;
     uint32_t *am_i;
     uint64_t *prof;          // optional: wall-clock stamp at kernel start, then after every phase

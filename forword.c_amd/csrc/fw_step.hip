@@ -134,64 +134,75 @@ __device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *
     for (uint32_t j = tid(); j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * w[j]) * scale;
 }
 
-// xs <- src (n floats, n even, optionally RMS-normalised by weights nw), src
-// published by other workgroups.  The loads go out in batches (8-byte
-// system-scope loads for src, plain loads for nw in the same batch), so
-// staging costs one memory round trip per batch.
-__device__ __forceinline__ void stage(float *xs, const float *src, uint32_t n, const float *nw, float eps, float *s_red)
+// xs <- src: n values published by other workgroups as {value, tag} words,
+// RMS-normalised by weights nw when given (rms_norm, norm.c:7-16).  Every
+// thread issues its loads at once and then calls issue() (this phase's first
+// weight items, which queue behind them).  Values whose tag is not yet `tag`
+// are loaded again, in batches with a back-off so early workgroups do not
+// flood memory.  Returns false when a wait gives up or another workgroup has
+// failed (the error word is then set); every thread returns the same.
+constexpr int MK_TB = 16;                   // values per thread per batch
+
+template <typename F>
+__device__ __forceinline__ bool stage(const MkArgs &a, float *xs, const uint64_t *src, uint32_t n, const float *nw,
+                                      float eps, uint32_t tag, float *s_red, uint32_t *s_fail, F &&issue)
 {
-    constexpr int B = 4096 / MK_THREADS;                 // 4096 float2 per batch
-    const uint32_t n2 = n / 2;
-    if (nw && n2 <= B * MK_THREADS) {                    // one batch: x and its norm weights together
-        const FW_GLOBAL float2v *w2 = reinterpret_cast<const FW_GLOBAL float2v *>(gptr(nw));
-        float2v v[B], w[B];
-#pragma unroll
-        for (int b = 0; b < B; b++) {
-            const uint32_t j = tid() + b * MK_THREADS;
-            if (j < n2) { v[b] = ld_sys2(src + 2 * j); w[b] = w2[j]; }
-        }
-        float ss = 0.f;
-#pragma unroll
-        for (int b = 0; b < B; b++)
-            if (tid() + b * MK_THREADS < n2) {
-                ss = __builtin_fmaf(v[b][0], v[b][0], ss);
-                ss = __builtin_fmaf(v[b][1], v[b][1], ss);
-            }
-        ss = block_sum_all(ss, s_red);
-        const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
-#pragma unroll
-        for (int b = 0; b < B; b++) {
-            const uint32_t j = tid() + b * MK_THREADS;
-            if (j < n2) {
-                float2v o;
-                o[0] = (v[b][0] * w[b][0]) * scale;
-                o[1] = (v[b][1] * w[b][1]) * scale;
-                *reinterpret_cast<float2v *>(xs + swz(2 * j)) = o;           // 2j, 2j+1 stay adjacent
-            }
-        }
-        __syncthreads();
-        return;
-    }
+    const uint32_t t = tid();
     float ss = 0.f;
-    for (uint32_t j0 = tid(); j0 < n2; j0 += 2 * B * MK_THREADS) {
-        float2v v[2 * B];
+    bool ok = true;
+    issue();
+    for (uint32_t j0 = 0; j0 < n; j0 += MK_TB * MK_THREADS) {
+        uint64_t v[MK_TB];
+        float w[MK_TB];
 #pragma unroll
-        for (int b = 0; b < 2 * B; b++) {
-            const uint32_t j = j0 + b * MK_THREADS;
-            if (j < n2) v[b] = ld_sys2(src + 2 * j);
+        for (int b = 0; b < MK_TB; b++) {
+            const uint32_t j = j0 + t + b * MK_THREADS;
+            v[b] = (uint64_t)tag << 32;
+            w[b] = 1.0f;
+            if (j < n) {
+                v[b] = ld_sys64(src + j);
+                if (nw) w[b] = gptr(nw)[j];
+            }
+        }
+        uint32_t stale = 0;
+#pragma unroll
+        for (int b = 0; b < MK_TB; b++)
+            if ((uint32_t)(v[b] >> 32) != tag) stale |= 1u << b;
+        for (uint32_t round = 0; stale && ok; round++) {
+            __builtin_amdgcn_s_sleep(8);                           // ~512 cycles
+            if (round > (1u << 16) || ((round & 15) == 15 && ld_sys(a.err) != 0)) {
+                ok = false;
+                break;
+            }
+#pragma unroll
+            for (int b = 0; b < MK_TB; b++)
+                if (stale & (1u << b)) v[b] = ld_sys64(src + j0 + t + b * MK_THREADS);
+#pragma unroll
+            for (int b = 0; b < MK_TB; b++)
+                if ((stale & (1u << b)) && (uint32_t)(v[b] >> 32) == tag) stale &= ~(1u << b);
         }
 #pragma unroll
-        for (int b = 0; b < 2 * B; b++) {
-            const uint32_t j = j0 + b * MK_THREADS;
-            if (j < n2) {
-                *reinterpret_cast<float2v *>(xs + swz(2 * j)) = v[b];
-                ss = __builtin_fmaf(v[b][0], v[b][0], ss);
-                ss = __builtin_fmaf(v[b][1], v[b][1], ss);
+        for (int b = 0; b < MK_TB; b++) {
+            const uint32_t j = j0 + t + b * MK_THREADS;
+            if (j < n) {
+                const float x = __builtin_bit_cast(float, (uint32_t)v[b]);
+                ss = __builtin_fmaf(x, x, ss);
+                xs[swz(j)] = x * w[b];                             // (x * w) * scale below (norm.c order)
             }
         }
     }
-    if (nw) norm_staged(xs, n, nw, eps, ss, s_red);
+    if (!ok) *s_fail = 1;
+    if (nw) {
+        ss = block_sum_all(ss, s_red);                             // also orders the stores above
+        const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
+        for (uint32_t j = t; j < n; j += MK_THREADS) xs[swz(j)] *= scale;
+    }
     __syncthreads();
+    if (*s_fail) {
+        if (t == 0) atomicOr(a.err, 1u);
+        return false;
+    }
+    return true;
 }
 
 // ── GEMV phase ───────────────────────────────────────────────────────────────
@@ -437,11 +448,26 @@ __device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t s
     const uint32_t pair = sl * m.P + m.ps;
     sx0 = sx1 = 0.f;
     if (pair < m.n_pairs) {
-        const float *xp = xs + 64 * (size_t)pair;
+        // Read through inline asm: for compiler-visible LDS reads the compiler
+        // cannot tell xs from the weight rings and first waits for every DMA
+        // in flight (the prefetched items of this phase).
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)(xs + 64 * (size_t)pair);
+        uint32_t ad[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) ad[i] = base + (((i + pair) & 15u) << 4);
+        float4v r[16];
+#pragma unroll
+        for (int q = 0; q < 16; q += 4)
+            asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\tds_read_b128 %3, %7"
+                         : "=&v"(r[q]), "=&v"(r[q + 1]), "=&v"(r[q + 2]), "=&v"(r[q + 3])
+                         : "v"(ad[q]), "v"(ad[q + 1]), "v"(ad[q + 2]), "v"(ad[q + 3]));
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                       "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]),
+                       "+v"(r[15]));
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float4 v = *reinterpret_cast<const float4 *>(xp + (((i + pair) & 15u) << 2));
-            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            xv[4 * i] = r[i][0]; xv[4 * i + 1] = r[i][1]; xv[4 * i + 2] = r[i][2]; xv[4 * i + 3] = r[i][3];
         }
         if constexpr (T != kQ8_0) {
             float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -613,7 +639,7 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
 // workgroup keeps its own rows of x in LDS (x_own), publishes the sums and
 // records the trace row.
 __device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, const float *part, float *x_own,
-                                          float *trace_row)
+                                          float *trace_row, uint32_t tag)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
@@ -622,7 +648,7 @@ __device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, cons
         const uint32_t r = lo + rl;
         const float v = x_own[rl] + row_sum<1>(part, rl, 0, ns);
         x_own[rl] = v;
-        st_sys(a.x + r, v);
+        st_sys64(a.tx + r, tagged(v, tag));
         st_sys(trace_row + r, v);
     }
 }
@@ -638,13 +664,13 @@ __device__ __forceinline__ float silu_f(float v)
 }
 
 // h = silu(gate x) * (up x) (ffn.c:82-104).
-__device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part)
+__device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part, uint32_t tag)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices(g.n_cols);
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS)
-        st_sys(a.h + lo + rl, silu_f(row_sum<2>(part, rl, 0, ns)) * row_sum<2>(part, rl, 1, ns));
+        st_sys64(a.th + lo + rl, tagged(silu_f(row_sum<2>(part, rl, 0, ns)) * row_sum<2>(part, rl, 1, ns), tag));
 }
 
 __device__ __forceinline__ bool am_better_mk(float v1, uint32_t i1, float v2, uint32_t i2)
@@ -873,10 +899,10 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
     __syncthreads();
 }
 
-// Merge the splits of KV head kvh's G query heads into a.att: every split's
+// Merge the splits of KV head kvh's G query heads into a.tatt (tagged): every split's
 // (m, l) in one batch of loads, then each thread's o values in batches of 32.
 template <int EPL, int G>
-__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds)
+__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds, uint32_t tag)
 {
     constexpr int HD = 32 * EPL, SB = 32;
     const uint32_t ns = a.n_splits;
@@ -919,13 +945,13 @@ __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, floa
             for (int k = 0; k < SB; k++)
                 if (s0 + k < ns) O = __builtin_fmaf(v[k], w[s0 + k], O);
         }
-        st_sys(a.att + (size_t)(kvh * G + g) * HD + d, O * s_inv[g]);
+        st_sys64(a.tatt + (size_t)(kvh * G + g) * HD + d, tagged(O * s_inv[g], tag));
     }
     __syncthreads();
 }
 
 template <int EPL, int G>
-__device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds)
+__device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
 {
     __shared__ uint32_t s_last;
     const uint32_t items = a.n_kv * a.n_splits;
@@ -935,29 +961,29 @@ __device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uin
         if (tid() == 0) s_last = ticket_sys(a.tickets + kvh) == a.n_splits - 1;
         __syncthreads();
         if (s_last) {
-            attn_combine<EPL, G>(a, kvh, lds);
+            attn_combine<EPL, G>(a, kvh, lds, tag);
             if (tid() == 0) st_sys(a.tickets + kvh, 0u);
         }
     }
 }
 
 template <int EPL>
-__device__ __forceinline__ void attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds)
+__device__ __forceinline__ void attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
 {
     switch (a.n_head / a.n_kv) {
-    case 1: attention_t<EPL, 1>(a, layer, pos, lds); break;
-    case 2: attention_t<EPL, 2>(a, layer, pos, lds); break;
-    case 4: attention_t<EPL, 4>(a, layer, pos, lds); break;
-    default: attention_t<EPL, 8>(a, layer, pos, lds); break;
+    case 1: attention_t<EPL, 1>(a, layer, pos, lds, tag); break;
+    case 2: attention_t<EPL, 2>(a, layer, pos, lds, tag); break;
+    case 4: attention_t<EPL, 4>(a, layer, pos, lds, tag); break;
+    default: attention_t<EPL, 8>(a, layer, pos, lds, tag); break;
     }
 }
 
-__device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds)
+__device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
 {
     switch (a.head_dim) {
-    case 32: attention_e<1>(a, layer, pos, lds); break;
-    case 64: attention_e<2>(a, layer, pos, lds); break;
-    default: attention_e<4>(a, layer, pos, lds); break;
+    case 32: attention_e<1>(a, layer, pos, lds, tag); break;
+    case 64: attention_e<2>(a, layer, pos, lds, tag); break;
+    default: attention_e<4>(a, layer, pos, lds, tag); break;
     }
 }
 
@@ -1059,7 +1085,7 @@ __device__ __forceinline__ uint32_t phase_kind(const MkArgs &a, uint32_t i)
 }
 
 // Embedding row (transformer.c:168-182) into the staging area, RMS-normalised
-// for the first QKV; the workgroup's own rows also go to x_own and x.
+// for the first QKV; the workgroup's own rows also go to x_own.
 __device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, uint32_t tok, const float *nw,
                                       float *s_red)
 {
@@ -1074,10 +1100,7 @@ __device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, 
         if (a.embd_scale != 1.0f) v *= a.embd_scale;
         xs[swz(j)] = v;
         ss = __builtin_fmaf(v, v, ss);
-        if (j >= lo && j < hi) {
-            x_own[j - lo] = v;
-            st_sys(a.x + j, v);
-        }
+        if (j >= lo && j < hi) x_own[j - lo] = v;
     }
     norm_staged(xs, a.n_embd, nw, a.eps, ss, s_red);
     __syncthreads();
@@ -1107,6 +1130,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     uint32_t epoch = a.epoch0;
     uint32_t n_pre = 0;                       // items of this wave's next matrix phase in flight
     const bool stamp = a.prof && blockIdx.x == 0 && tid() == 0;
+    if (tid() == 0) s_fail = 0;
     if (stamp) a.prof[0] = wall_clock64();
     __syncthreads();
     for (uint32_t step = 0; step < a.n_steps; step++) {
@@ -1120,8 +1144,9 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
 
         for (uint32_t i = 0; i < n_ops; i++) {
             const uint32_t kind = phase_kind(a, i), layer = i / 5;
+            const uint32_t tag_out = epoch + 1;                // tag of the values this phase publishes
             if (kind == MK_ATTN) {
-                attention(a, layer, pos, lds);
+                attention(a, layer, pos, lds, tag_out);
             } else if (kind == MK_HEAD && skip_head) {
                 if (blockIdx.x == 0 && tid() == 0) {
                     st_sys(&a.state->token, a.prompt[pos + 1]);
@@ -1129,40 +1154,48 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 }
             } else {
                 // one call site per GEMV variant keeps the executed code small
-                const float *src = kind == MK_WO ? a.att : kind == MK_DOWN ? a.h : a.x;
+                const uint64_t *src = kind == MK_WO ? a.tatt : kind == MK_DOWN ? a.th : a.tx;
                 const uint32_t n_in = kind == MK_DOWN ? a.n_ff : a.n_embd;
                 const float *nw = kind == MK_QKV ? uni(tab[layer].attn_norm)
                                 : kind == MK_FFN ? uni(tab[layer].ffn_norm)
                                 : kind == MK_HEAD ? a.out_norm : nullptr;
-                if (kind == MK_QKV && layer == 0) embed(a, xs, x_own, tok, nw, s_red);
-                else stage(xs, src, n_in, nw, a.eps, s_red);
                 const MkGemv g = phase_gemv(a, tab, kind, layer);
+                if (kind == MK_QKV && layer == 0) {
+                    embed(a, xs, x_own, tok, nw, s_red);
+                } else {
+                    // the phase's first weight items go out right behind the input loads
+                    auto issue = [&]() {
+                        if (n_pre) return;
+                        if (kind == MK_FFN) n_pre = prefetch<TL, 2>(g, lds8, lay.fixed, lay.attn);
+                        else if (kind == MK_HEAD) n_pre = prefetch<TH, 1>(g, lds8, lay.fixed, lay.attn);
+                        else n_pre = prefetch<TL, 1>(g, lds8, lay.fixed, lay.attn);
+                    };
+                    if (!stage(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue)) return;
+                }
                 if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 else gemv<TL, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 if (kind == MK_QKV) epi_qkv(a, g, part, rope, layer, pos);
-                else if (kind == MK_FFN) epi_swiglu(a, g, part);
+                else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out);
                 else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
-                else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd);
+                else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd, tag_out);
                 n_pre = 0;
             }
-            bar_arrive(a, epoch + 1, &s_fail);
-            // the first items of the next matrix phase (past attention), in flight across the barrier
-            if (kind != MK_ATTN) {
+            // Grid barriers only before attention (it reads the KV row just
+            // appended) and at the end of a step (the next token); the other
+            // phases wait for their tagged inputs instead.
+            if (kind == MK_QKV || i + 1 == n_ops) {
+                bar_arrive(a, tag_out, &s_fail);
+                // the next matrix phase's first items, in flight across the barrier
                 const bool wrap = i + 1 == n_ops;
                 if (!wrap || step + 1 < a.n_steps) {
-                    uint32_t ni = wrap ? 0 : i + 1;
-                    if (phase_kind(a, ni) == MK_ATTN) ni++;
-                    const uint32_t nk = phase_kind(a, ni);
-                    if (!(nk == MK_HEAD && skip_head)) {
-                        const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
-                        if (nk == MK_FFN) n_pre = prefetch<TL, 2>(ng, lds8, lay.fixed, lay.attn);
-                        else if (nk == MK_HEAD) n_pre = prefetch<TH, 1>(ng, lds8, lay.fixed, lay.attn);
-                        else n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);
-                    }
+                    const uint32_t ni = wrap ? 0 : i + 2, nk = phase_kind(a, ni);   // past attention
+                    const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
+                    n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);        // WO, or the first QKV
                 }
+                if (!bar_wait(a, tag_out, &s_fail)) return;
             }
-            if (!bar_wait(a, ++epoch, &s_fail)) return;
+            epoch = tag_out;
             if (stamp) a.prof[1 + step * n_ops + i] = wall_clock64();
         }
     }
