@@ -783,6 +783,9 @@ extern "C" int forword_gpu_quant_matvec(const void *weights, size_t weights_size
         set_err("quant_matvec: weights buffer too small or sizes too large");
         return -1;
     }
+    const hipError_t e = launch_gemv(type, (const uint8_t *)weights, rb, input, output, (uint32_t)out, (uint32_t)in,
+                                     (hipStream_t)stream);
+    if (e != hipErrorNotSupported) return launched(e, "quant_matvec");
     QmvArgs a{};
     a.n_seg = 1; a.w[0] = (const uint8_t *)weights; a.rows[0] = (uint32_t)out; a.n_cols = (uint32_t)in;
     a.row_bytes = rb; a.x = input; a.out[0] = output;
