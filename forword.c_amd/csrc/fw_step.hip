@@ -20,14 +20,16 @@
 // then LM-HEAD (output RMSNorm folded in) with the argmax reduced by a ticket.
 //
 // GEMV mapping.  A phase's rows are split evenly (even counts, so RoPE pairs
-// stay together) over the workgroups.  Columns are cut into at most eight
-// slices of P block pairs (P a power of two); each wave owns a slice, its
-// lanes are (row-in-group, pair) = (lane / P, lane % P), so one item of the
-// wave's weight stream covers 64/P rows.  A lane keeps the 64 input values of
-// its pair in registers for the whole slice, so a wave reads only P distinct
-// 64-float blocks of the LDS-staged input (stored with a per-block rotation
-// of its 16-byte chunks so those reads are bank-conflict free).  Per-row
-// partial sums of the slices go through LDS and are added in slice order.
+// stay together) over the workgroups.  Columns are cut into (at most eight
+// per wave set) slices of Q block pairs, Q = pairs / 8 rounded up, so the
+// waves get equal shares; each wave owns a slice, its lanes are (row-in-group,
+// pair) = (lane / P, lane % P) with P the power of two >= Q (lanes past Q only
+// reload the slice's last pair), so one item of the wave's weight stream
+// covers 64/P rows.  A lane keeps the 64 input values of its pair in
+// registers for the whole slice, so a wave reads only Q distinct 64-float
+// blocks of the LDS-staged input (stored with a per-block rotation of its
+// 16-byte chunks so those reads are bank-conflict free).  Per-row partial
+// sums of the slices go through LDS and are added in slice order.
 //
 // Cross-workgroup data (activations, partials, tickets, flags, step state)
 // moves through system-scope relaxed atomics: the L2s of the eight XCDs are not
@@ -214,24 +216,32 @@ __host__ __device__ inline uint32_t mk_rows_per_wg(uint32_t n_rows, uint32_t n_w
     return (per + 1) & ~1u;
 }
 
-__host__ __device__ inline uint32_t pairs_per_slice(uint32_t n_pairs)
+// Block pairs per column slice: the pairs of a row spread evenly over the
+// waves (at most 64 per slice).
+__host__ __device__ inline uint32_t slice_pairs(uint32_t n_pairs)
 {
-    const uint32_t need = (n_pairs + MK_WAVES - 1) / MK_WAVES;
+    const uint32_t q = (n_pairs + MK_WAVES - 1) / MK_WAVES;
+    return q < 1 ? 1 : q > 64 ? 64 : q;
+}
+
+// Lanes per row group: the power of two that holds a slice's pairs.
+__host__ __device__ inline uint32_t lanes_per_row(uint32_t q)
+{
     uint32_t p = 1;
-    while (p < need && p < 64) p <<= 1;
+    while (p < q) p <<= 1;
     return p;
 }
 
 // Column slices of a row of n_cols values.
 __host__ __device__ inline uint32_t n_slices(uint32_t n_cols)
 {
-    const uint32_t np = n_cols / 64, p = pairs_per_slice(np);
-    return (np + p - 1) / p;
+    const uint32_t np = n_cols / 64, q = slice_pairs(np);
+    return (np + q - 1) / q;
 }
 
 struct Map {
     uint32_t lo, hi;          // rows of this workgroup
-    uint32_t P, S;            // pairs per slice, slices (<= MK_SMAX)
+    uint32_t Q, P, S;         // pairs per slice, lanes per row (power of two >= Q), slices
     uint32_t slice, sstep;    // this wave's first slice and the stride to its next one
     uint32_t wis, nws;        // this wave's index among its slice's waves, their count
     uint32_t ps, rs;          // this lane's pair in the slice, row in the group
@@ -247,8 +257,9 @@ __device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols)
     m.lo = min(n_rows, blockIdx.x * per);
     m.hi = min(n_rows, m.lo + per);
     m.n_pairs = n_cols / 64;
-    m.P = pairs_per_slice(m.n_pairs);
-    m.S = (m.n_pairs + m.P - 1) / m.P;
+    m.Q = slice_pairs(m.n_pairs);
+    m.P = lanes_per_row(m.Q);
+    m.S = (m.n_pairs + m.Q - 1) / m.Q;
     const uint32_t wave = wave_id(), lane = tid() & 63;
     if (m.S <= (uint32_t)MK_WAVES) {
         m.slice = wave % m.S;
@@ -390,7 +401,7 @@ template <uint32_t T, int M>
 __device__ __forceinline__ void dma_item(const MkGemv &g, const Map &m, const Cur &c, uint8_t *ring)
 {
     const uint32_t sl = m.slice + c.si * m.sstep;
-    const uint32_t pair = min(sl * m.P + m.ps, m.n_pairs - 1);
+    const uint32_t pair = min(sl * m.Q + min(m.ps, m.Q - 1), m.n_pairs - 1);   // lanes past Q reload the last
     const uint32_t r = min(map_row(m, c.k), m.hi - 1);
     uint8_t *slot = ring + c.slot * slot_bytes(T, M);
 #pragma unroll
@@ -445,9 +456,9 @@ template <uint32_t T>
 __device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t sl, float (&xv)[64], float &sx0,
                                        float &sx1)
 {
-    const uint32_t pair = sl * m.P + m.ps;
+    const uint32_t pair = sl * m.Q + m.ps;
     sx0 = sx1 = 0.f;
-    if (pair < m.n_pairs) {
+    if (m.ps < m.Q && pair < m.n_pairs) {
         // Read through inline asm: for compiler-visible LDS reads the compiler
         // cannot tell xs from the weight rings and first waits for every DMA
         // in flight (the prefetched items of this phase).
@@ -562,7 +573,7 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
         const uint32_t sl = m.slice + si * m.sstep;
         float xv[64], sx0, sx1;
         load_x<T>(xs, m, sl, xv, sx0, sx1);
-        const bool pair_on = sl * m.P + m.ps < m.n_pairs;
+        const bool pair_on = m.ps < m.Q && sl * m.Q + m.ps < m.n_pairs;
         for (uint32_t k = 0; k < m.n_my; k++, it++) {
             wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
             uint32_t dw[M][NDW];
