@@ -776,6 +776,15 @@ __device__ __forceinline__ void load_vec(const FW_GLOBAL float *p, float (&v)[EP
     }
 }
 
+// Splits of the positions 0..pos per KV head in this step: about one per 64
+// positions, at most the n_splits the partial buffer holds.  Short contexts
+// then have fewer, longer items and a cheaper combine.
+__device__ __forceinline__ uint32_t attn_splits_at(const MkArgs &a, uint32_t pos)
+{
+    const uint32_t want = (pos + 64) / 64;
+    return want > a.n_splits ? a.n_splits : want;
+}
+
 // Positions t = first, first + NG, ... below t1 (NG = 2 * MK_WAVES) into the
 // running (m, l, o) of the G heads: a batch of U positions is loaded at once
 // (positions past t1 reload the batch's first one and get no weight), all
@@ -841,7 +850,7 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
     float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
     float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
     float (*s_l)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD + MK_WAVES * G);
-    const uint32_t n_pos = pos + 1, ns = a.n_splits, chunk = (n_pos + ns - 1) / ns;
+    const uint32_t n_pos = pos + 1, ns = attn_splits_at(a, pos), chunk = (n_pos + ns - 1) / ns;
     const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
     const int lane = tid() & 63, wave = wave_id(), grp = lane >> 5, l32 = lane & 31;
     const size_t kvd = (size_t)a.n_kv * HD;
@@ -913,10 +922,10 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
 // Merge the splits of KV head kvh's G query heads into a.tatt (tagged): every split's
 // (m, l) in one batch of loads, then each thread's o values in batches of 32.
 template <int EPL, int G>
-__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds, uint32_t tag)
+__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds, uint32_t tag, uint32_t pos)
 {
     constexpr int HD = 32 * EPL, SB = 32;
-    const uint32_t ns = a.n_splits;
+    const uint32_t ns = attn_splits_at(a, pos);
     float *s_w = lds;                                      // [G][ns] m, then the split weights
     float *s_l = lds + G * ns;                             // [G][ns] l
     float *s_inv = lds + 2 * G * ns;                       // [G] 1 / sum of weights
@@ -965,14 +974,14 @@ template <int EPL, int G>
 __device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
 {
     __shared__ uint32_t s_last;
-    const uint32_t items = a.n_kv * a.n_splits;
+    const uint32_t items = a.n_kv * attn_splits_at(a, pos);
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint32_t kvh = it % a.n_kv, split = it / a.n_kv;
         attn_item<EPL, G>(a, layer, pos, kvh, split, lds);
-        if (tid() == 0) s_last = ticket_sys(a.tickets + kvh) == a.n_splits - 1;
+        if (tid() == 0) s_last = ticket_sys(a.tickets + kvh) == attn_splits_at(a, pos) - 1;
         __syncthreads();
         if (s_last) {
-            attn_combine<EPL, G>(a, kvh, lds, tag);
+            attn_combine<EPL, G>(a, kvh, lds, tag, pos);
             if (tid() == 0) st_sys(a.tickets + kvh, 0u);
         }
     }
