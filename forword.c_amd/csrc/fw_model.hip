@@ -288,9 +288,13 @@ static int mk_check(forword_gpu_t *h)
     uint32_t err = 0;
     HIPCHK(hipMemcpy(&err, h->d_mk_err, 4, hipMemcpyDeviceToHost), "persistent step status");
     if (!err) return 0;
+    // the epoch restarts at 0, so every flag and tagged word goes back to 0 too
     (void)hipMemset(h->d_bar, 0, (size_t)h->mk_wg * 128);
     (void)hipMemset(h->d_mk_tickets, 0, 64 * 4);
     (void)hipMemset(h->d_mk_err, 0, 4);
+    (void)hipMemset(h->d_tx, 0, (size_t)h->cfg.n_embd * 8);
+    (void)hipMemset(h->d_tatt, 0, (size_t)h->cfg.n_embd * 8);
+    (void)hipMemset(h->d_th, 0, (size_t)h->cfg.n_ff * 8);
     (void)hipDeviceSynchronize();
     h->mk_epoch = 0;
     set_err("persistent step kernel: a grid barrier timed out; results of the last call are invalid");

@@ -381,17 +381,36 @@ __device__ __forceinline__ void advance(Cur &c, uint32_t n_my, uint32_t ns)
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// One LDS-DMA load of BYTES per lane (global_load_lds): lane i's bytes land at
+// LDS byte lds + BYTES * i.  Issued through inline asm: the compiler treats
+// the builtin's address registers as busy until the load completes and waits
+// for every load in flight before reusing them, which serialises a ring fill.
+// The ring's waits are explicit (wait_items), so nothing depends on the
+// compiler's accounting.  M0 (reserved by the compiler) is saved and
+// restored; it is written one instruction ahead of the load that reads it.
+#define FW_DMA_LDS(INSN)                                                                                 \
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t" INSN " %1, off\n\ts_mov_b32 m0, %0" \
+                 : "=&s"(keep)                                                                            \
+                 : "v"(src), "s"(m)                                                                       \
+                 : "memory")
+template <int BYTES>
+__device__ __forceinline__ void dma_lds(const FW_GLOBAL uint8_t *src, uint8_t *lds)
+{
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)lds);
+    uint32_t keep;
+    if constexpr (BYTES == 16) FW_DMA_LDS("global_load_lds_dwordx4");
+    else if constexpr (BYTES == 12) FW_DMA_LDS("global_load_lds_dwordx3");
+    else FW_DMA_LDS("global_load_lds_dword");
+}
+#undef FW_DMA_LDS
+
 template <uint32_t T>
 __device__ __forceinline__ void dma_pair(const uint8_t *src, uint8_t *dst)
 {
     const FW_GLOBAL uint8_t *s = gptr(src);
 #pragma unroll
-    for (uint32_t i = 0; i < dma_n16(T); i++)
-        __builtin_amdgcn_global_load_lds((const FW_GLOBAL void *)(s + 16 * i), (lds_void *)(dst + 1024 * i), 16, 0, 0);
-    const FW_GLOBAL void *ts = s + 16 * dma_n16(T);
-    lds_void *td = (lds_void *)(dst + 1024 * dma_n16(T));
-    if constexpr (dma_tail(T) == 12) __builtin_amdgcn_global_load_lds(ts, td, 12, 0, 0);
-    else __builtin_amdgcn_global_load_lds(ts, td, 4, 0, 0);
+    for (uint32_t i = 0; i < dma_n16(T); i++) dma_lds<16>(s + 16 * i, dst + 1024 * i);
+    dma_lds<(int)dma_tail(T)>(s + 16 * dma_n16(T), dst + 1024 * dma_n16(T));
 }
 
 // Issue item c.  Every load is issued: a row past the workgroup's last one and
@@ -1207,8 +1226,10 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
             if (kind == MK_QKV || i + 1 == n_ops) {
                 bar_arrive(a, tag_out, &s_fail);
                 // the next matrix phase's first items, in flight across the barrier
+                // (not by a workgroup with an attention item: its KV loads
+                // would queue behind these DMAs)
                 const bool wrap = i + 1 == n_ops;
-                if (!wrap || step + 1 < a.n_steps) {
+                if (wrap ? step + 1 < a.n_steps : blockIdx.x >= a.n_kv * attn_splits_at(a, pos)) {
                     const uint32_t ni = wrap ? 0 : i + 2, nk = phase_kind(a, ni);   // past attention
                     const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
                     n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);        // WO, or the first QKV
