@@ -67,6 +67,9 @@ bool qmv_pair_ok(uint32_t type, uint32_t n_cols, const void *base);
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n, float eps,
                           hipStream_t s);
+// RMSNorm of `rows` consecutive rows of n floats (one workgroup each).
+hipError_t launch_rmsnorm_rows(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps,
+                               hipStream_t s);
 hipError_t launch_embed(const uint8_t *w, uint32_t type, uint32_t n_cols, uint32_t n_rows,
                         const StepState *st, const uint32_t *token_override, float embd_scale, float *x,
                         float *scale_out, float norm_eps, hipStream_t s);
@@ -93,4 +96,22 @@ hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t 
 hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);
 
+// Batched prompt forward (fw_prefill.hip).
+// Y[t][r] (+)= Σ_k X[t][k]·W[r][k] for t < n_tok, r < n_out: X fp32 rows ldx
+// apart, W Q4_0/Q5_0/Q8_0 rows of n_in columns, Y rows ldy apart.
+hipError_t launch_gemm_q(uint32_t type, const float *x, uint32_t ldx, const uint8_t *w, uint64_t row_bytes, float *y,
+                         uint32_t ldy, uint32_t n_tok, uint32_t n_out, uint32_t n_in, bool accumulate,
+                         hipStream_t s);
+// X[t] = embedding row tokens[t] (times embd_scale when it is not 1).
+hipError_t launch_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols, const uint32_t *tokens,
+                             uint32_t n_tok, float embd_scale, float *x, hipStream_t s);
+// Rows [q | k | v] ld floats apart at positions pos0..: RoPE on q in place, K
+// (rotated) and V appended to the layer's cache rows.
+hipError_t launch_rope_append(float *qkv, uint32_t ld, uint32_t n_tok, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                              uint32_t pos0, const float *cos_tab, const float *sin_tab, float *kc_layer,
+                              float *vc_layer, hipStream_t s);
+// Causal attention of the n_tok rows' queries over cache rows 0..pos0+t.
+hipError_t launch_attn_prefill(const float *qkv, uint32_t ld, uint32_t n_tok, const float *kc_layer,
+                               const float *vc_layer, float *out, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                               uint32_t pos0, hipStream_t s);
 } // namespace fw

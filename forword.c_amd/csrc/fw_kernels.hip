@@ -290,6 +290,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
 {
     extern __shared__ float s_x[];                 // x staged once (n <= 16384), else read from global
     __shared__ float s_scale;
+    x += (size_t)blockIdx.x * n;                   // one row per workgroup
+    out += (size_t)blockIdx.x * n;
     const bool staged = n <= 16384;
     if (staged) {
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) s_x[i] = x[i];
@@ -337,8 +339,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, uint32_t n, float eps, hipStream_t s)
 {
+    return launch_rmsnorm_rows(x, w, out, n, 1, eps, s);
+}
+
+hipError_t launch_rmsnorm_rows(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps,
+                               hipStream_t s)
+{
     size_t lds = n <= 16384 ? (size_t)n * 4 : 0;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), lds, s, x, w, out, n, eps);
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), lds, s, x, w, out, n, eps);
     return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@
 #include "forword_gpu.h"
 
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <math.h>
 #include <mutex>
 #include <stdarg.h>
@@ -109,6 +110,9 @@ struct forword_gpu {
     MkLayer *d_layers = nullptr;
     uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
     uint32_t prof_steps = 0;
+    // batched prefill: activations of up to kPrefillChunk tokens (allocated on first use)
+    float *d_pf = nullptr;
+    uint32_t *d_pf_tok = nullptr;
     std::vector<void *> allocs;
 };
 
@@ -664,6 +668,108 @@ extern "C" int forword_gpu_decode_from(forword_gpu_t *h, uint32_t token, size_t 
         HIPCHK(hipStreamSynchronize(h->stream), "decode_from");
         if (mk_check(h)) return -1;
     }
+    return 0;
+}
+
+// ── batched prefill ──────────────────────────────────────────────────────────
+
+// Tokens per pass of the batched prefill: longer prompts run in passes, each
+// attending to the cache rows the previous ones wrote.
+static constexpr uint32_t kPrefillChunk = 512;
+
+static bool prefill_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
+
+// Queue the batched forward of tokens[0..n_tok) at positions pos0.. (KV rows
+// written), the last token's logits into d_logits and their argmax into d_argmax.
+static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, size_t pos0)
+{
+    if (!h || !tokens || !n_tok) { set_err("prefill: invalid arguments"); return -1; }
+    const forword_gpu_config_t &c = h->cfg;
+    if (pos0 > h->n_ctx || n_tok > h->n_ctx - pos0) {
+        set_err("prefill: positions [%zu, %zu) exceed the KV cache (%zu)", pos0, pos0 + n_tok, h->n_ctx);
+        return -1;
+    }
+    for (size_t i = 0; i < n_tok; i++)
+        if (tokens[i] >= c.n_vocab) { set_err("prefill: token %u out of range", tokens[i]); return -1; }
+    const uint32_t n = c.n_embd, hd = c.head_dim, nq = c.n_head * hd, kvd = c.n_head_kv * hd, nff = c.n_ff;
+    for (const Layer &Ly : h->L)
+        for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })
+            if (!prefill_type_ok(l->type)) { set_err("prefill: linear type %u not supported", l->type); return -1; }
+    if (!attn_supported(hd, c.n_head / std::max<uint32_t>(c.n_head_kv, 1)) || c.n_head % c.n_head_kv || nq != n) {
+        set_err("prefill: head layout not supported");
+        return -1;
+    }
+    // per-token activations: x, xn [n] | q k v [nq + 2 kvd] | attention [nq] | gate, up [n_ff]
+    const size_t ldqkv = (size_t)nq + 2 * kvd, per_tok = 2 * (size_t)n + ldqkv + nq + 2 * (size_t)nff;
+    if (!h->d_pf && (dalloc(h, (void **)&h->d_pf, kPrefillChunk * per_tok * 4, "prefill activations") ||
+                     dalloc(h, (void **)&h->d_pf_tok, kPrefillChunk * 4, "prefill tokens")))
+        return -1;
+    float *X = h->d_pf, *Xn = X + (size_t)kPrefillChunk * n, *QKV = Xn + (size_t)kPrefillChunk * n;
+    float *Att = QKV + (size_t)kPrefillChunk * ldqkv, *G = Att + (size_t)kPrefillChunk * nq;
+    float *U = G + (size_t)kPrefillChunk * nff;
+    hipStream_t s = h->stream;
+#define TRY(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { set_err("prefill: %s (line %d)", hipGetErrorString(e_), __LINE__); return -1; } } while (0)
+    uint32_t rows = 0;
+    for (size_t c0 = 0; c0 < n_tok; c0 += kPrefillChunk) {
+        rows = (uint32_t)std::min<size_t>(kPrefillChunk, n_tok - c0);
+        const uint32_t p0 = (uint32_t)(pos0 + c0);
+        TRY(hipMemcpyAsync(h->d_pf_tok, tokens + c0, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+        TRY(launch_embed_rows(h->embd.w, h->embd.type, n, h->d_pf_tok, rows, c.embd_scale, X, s));
+        for (uint32_t l = 0; l < c.n_layer; l++) {
+            const Layer &Ly = h->L[l];
+            float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
+            TRY(launch_rmsnorm_rows(X, Ly.attn_norm, Xn, n, rows, c.norm_eps, s));            // transformer.c:255
+            TRY(launch_gemm_q(Ly.q.type, Xn, n, Ly.q.w, Ly.q.row_bytes, QKV, ldqkv, rows, nq, n, false, s));
+            TRY(launch_gemm_q(Ly.k.type, Xn, n, Ly.k.w, Ly.k.row_bytes, QKV + nq, ldqkv, rows, kvd, n, false, s));
+            TRY(launch_gemm_q(Ly.v.type, Xn, n, Ly.v.w, Ly.v.row_bytes, QKV + nq + kvd, ldqkv, rows, kvd, n, false, s));
+            TRY(launch_rope_append(QKV, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
+            TRY(launch_attn_prefill(QKV, ldqkv, rows, kc, vc, Att, c.n_head, c.n_head_kv, hd, p0, s));
+            TRY(launch_gemm_q(Ly.o.type, Att, nq, Ly.o.w, Ly.o.row_bytes, X, n, rows, n, nq, true, s));   // :271-272
+            TRY(launch_rmsnorm_rows(X, Ly.ffn_norm, Xn, n, rows, c.norm_eps, s));             // :275
+            TRY(launch_gemm_q(Ly.gate.type, Xn, n, Ly.gate.w, Ly.gate.row_bytes, G, nff, rows, nff, n, false, s));
+            TRY(launch_gemm_q(Ly.up.type, Xn, n, Ly.up.w, Ly.up.row_bytes, U, nff, rows, nff, n, false, s));
+            TRY(launch_silu_mul(G, U, G, (uint64_t)rows * nff, s));                           // ffn.c:95-103
+            TRY(launch_gemm_q(Ly.down.type, G, nff, Ly.down.w, Ly.down.row_bytes, X, n, rows, n, nff, true, s));
+        }
+    }
+    // logits of the last token (transformer.c:293-323), then its argmax
+    const float *xl = X + (size_t)(rows - 1) * n;
+    if (h->out_norm) TRY(launch_rmsnorm(xl, h->out_norm, h->d_xn, n, c.norm_eps, s));
+    else TRY(hipMemcpyAsync(h->d_xn, xl, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+    {
+        QmvArgs a{};
+        a.n_seg = 1; a.w[0] = h->out.w; a.rows[0] = h->out.out; a.n_cols = n; a.row_bytes = h->out.row_bytes;
+        a.x = h->d_xn; a.out[0] = h->d_logits; a.state = h->d_state;
+        qmv_plan(a, EPI_STORE);
+        TRY(launch_qmv(h->out.type, EPI_STORE, a, s));
+    }
+    TRY(launch_argmax(h->d_logits, c.n_vocab, h->d_pv, h->d_pi, h->d_counter, h->d_argmax, nullptr, nullptr, nullptr,
+                      h->am_blocks, s));
+#undef TRY
+    h->traced = false;                       // no per-layer trace of a batched pass
+    return 0;
+}
+
+extern "C" float *forword_gpu_prefill(forword_gpu_t *h, const uint32_t *tokens, size_t n_tokens, size_t pos0)
+{
+    if (prefill_run(h, tokens, n_tokens, pos0)) return nullptr;
+    if (hipMemcpyAsync(h->h_logits, h->d_logits, (size_t)h->cfg.n_vocab * 4, hipMemcpyDeviceToHost, h->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(h->stream) != hipSuccess) {
+        set_err("prefill: %s", hipGetErrorString(hipGetLastError()));
+        return nullptr;
+    }
+    return h->h_logits;
+}
+
+extern "C" int forword_gpu_prefill_argmax(forword_gpu_t *h, const uint32_t *tokens, size_t n_tokens, size_t pos0,
+                                          uint32_t *next)
+{
+    if (!next) { set_err("prefill_argmax: next is NULL"); return -1; }
+    if (prefill_run(h, tokens, n_tokens, pos0)) return -1;
+    HIPCHK(hipMemcpyAsync(h->h_u32, h->d_argmax, 4, hipMemcpyDeviceToHost, h->stream), "argmax download");
+    HIPCHK(hipStreamSynchronize(h->stream), "prefill_argmax");
+    *next = h->h_u32[0];
     return 0;
 }
 

@@ -1,0 +1,301 @@
+// Batched prompt forward (prefill).  forword.c feeds a prompt one token at a
+// time through transformer_forward (main.c:145-151), so every weight matrix is
+// read once per prompt token.  Here the prompt's tokens go through each layer
+// together: the linears are fp32 GEMMs on the matrix cores
+// (v_mfma_f32_16x16x4_f32) with the quantised weights dequantised exactly into
+// LDS, the rest are batched versions of the per-token kernels.  Same arithmetic
+// as the reference per element except the order of the linears' sums (the
+// matrix cores accumulate in their own order), so results agree within the
+// floating-point tolerance, not bit for bit.
+#include "fw_device.h"
+#include "fw_kernels.h"
+
+namespace fw {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ── GEMM: Y[t][r] = Σ_k X[t][k] · W[r][k] ───────────────────────────────────
+//
+// A workgroup computes a 64-token × 128-row tile; each of its 4 waves a 32×64
+// part of it as 2×4 tiles of 16×16.  K advances one quantisation block (32
+// columns) at a time: the 64×32 input tile and the 128 dequantised weight rows
+// are staged in LDS (rows padded to 33 floats against bank conflicts).
+// v_mfma_f32_16x16x4_f32 operands: lane l gives A[l%16][l/16] and B[l/16][l%16];
+// the result tile holds D[4·(l/16)+i][l%16] in element i of lane l.
+constexpr int PG_BM = 64, PG_BN = 128, PG_BK = 32, PG_THREADS = 256;
+
+template <uint32_t T>
+__global__ __launch_bounds__(PG_THREADS) void k_gemm_q(const float *__restrict__ X, uint32_t ldx,
+                                                       const uint8_t *__restrict__ W, uint64_t row_bytes,
+                                                       float *__restrict__ Y, uint32_t ldy, uint32_t n_tok,
+                                                       uint32_t n_out, uint32_t n_in, int accumulate)
+{
+    __shared__ float Xs[PG_BM][PG_BK + 1];
+    __shared__ float Ws[PG_BN][PG_BK + 1];
+    const uint32_t r0 = blockIdx.x * PG_BN, t0 = blockIdx.y * PG_BM;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    floatx4 acc[2][4];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 4; ni++) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // this thread's share of the weight tile: row wr, columns 16·wh .. 16·wh+15
+    const int wr = tid >> 1, wh = tid & 1;
+    const uint32_t r = r0 + wr;
+    const uint8_t *wrow = W + (size_t)min(r, n_out - 1) * row_bytes;
+    for (uint32_t k0 = 0; k0 < n_in; k0 += PG_BK) {
+#pragma unroll
+        for (int i = 0; i < PG_BM * PG_BK / PG_THREADS; i++) {
+            const int e = tid + i * PG_THREADS, m = e / PG_BK, k = e % PG_BK;
+            const uint32_t t = t0 + m;
+            Xs[m][k] = t < n_tok ? X[(size_t)t * ldx + k0 + k] : 0.f;
+        }
+        const uint8_t *blk = wrow + (size_t)(k0 / 32) * Blk<T>::bytes;
+#pragma unroll
+        for (int j = 0; j < 16; j++) Ws[wr][16 * wh + j] = r < n_out ? dequant_one(blk, T, 16 * wh + j) : 0.f;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < PG_BK; kk += 4) {
+            float a[2], b[4];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) a[mi] = Xs[wm * 32 + mi * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+            for (int ni = 0; ni < 4; ni++) b[ni] = Ws[wn * 64 + ni * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int ni = 0; ni < 4; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 4; ni++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t t = t0 + wm * 32 + mi * 16 + 4 * (lane >> 4) + i;
+                const uint32_t rr = r0 + wn * 64 + ni * 16 + (lane & 15);
+                if (t < n_tok && rr < n_out) {
+                    float *p = Y + (size_t)t * ldy + rr;
+                    *p = accumulate ? *p + acc[mi][ni][i] : acc[mi][ni][i];   // x[i] += y[i] (transformer.c:271-272)
+                }
+            }
+}
+
+hipError_t launch_gemm_q(uint32_t type, const float *x, uint32_t ldx, const uint8_t *w, uint64_t row_bytes, float *y,
+                         uint32_t ldy, uint32_t n_tok, uint32_t n_out, uint32_t n_in, bool accumulate,
+                         hipStream_t s)
+{
+    if (!n_tok || !n_out || !n_in || n_in % 32) return hipErrorInvalidValue;
+    const dim3 grid((n_out + PG_BN - 1) / PG_BN, (n_tok + PG_BM - 1) / PG_BM);
+    const int acc = accumulate ? 1 : 0;
+    switch (type) {
+    case kQ4_0: hipLaunchKernelGGL(k_gemm_q<kQ4_0>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc); break;
+    case kQ5_0: hipLaunchKernelGGL(k_gemm_q<kQ5_0>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc); break;
+    case kQ8_0: hipLaunchKernelGGL(k_gemm_q<kQ8_0>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc); break;
+    default: return hipErrorNotSupported;
+    }
+    return hipGetLastError();
+}
+
+// ── embedding rows, RMSNorm rows ────────────────────────────────────────────
+
+// X[t] = row tokens[t] of the embedding (linear_get_row, linear.c:60-151), times
+// embd_scale when it is not 1 (transformer.c:179-182).
+__global__ __launch_bounds__(256) void k_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols,
+                                                    const uint32_t *tokens, float embd_scale, float *X)
+{
+    const uint32_t t = blockIdx.y, tok = tokens[t];
+    const uint32_t j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= n_cols) return;
+    float v;
+    if (type == kF32) v = reinterpret_cast<const float *>(w)[(size_t)tok * n_cols + j];
+    else {
+        const uint32_t bb = block_bytes_dev(type);
+        v = dequant_one(w + (size_t)tok * (n_cols / 32) * bb + (size_t)(j / 32) * bb, type, j & 31);
+    }
+    if (embd_scale != 1.0f) v *= embd_scale;
+    X[(size_t)t * n_cols + j] = v;
+}
+
+hipError_t launch_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols, const uint32_t *tokens,
+                             uint32_t n_tok, float embd_scale, float *x, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_embed_rows, dim3((n_cols + 255) / 256, n_tok), dim3(256), 0, s, w, type, n_cols, tokens,
+                       embd_scale, x);
+    return hipGetLastError();
+}
+
+// ── RoPE on q and k, K/V append ─────────────────────────────────────────────
+
+// QKV[t] = [q (n_head·hd) | k (kvd) | v (kvd)] of token t at position pos0 + t:
+// rotate q in place and k (rope.c:37-43, interleaved pairs), append k and v to
+// the cache rows (attention.c:129-140).
+__global__ __launch_bounds__(256) void k_rope_append(float *qkv, uint32_t ld, uint32_t n_head, uint32_t n_kv,
+                                                     uint32_t hd, uint32_t pos0, const float *cos_tab,
+                                                     const float *sin_tab, float *kc, float *vc)
+{
+    const uint32_t t = blockIdx.y, half = hd / 2, pos = pos0 + t, kvd = n_kv * hd;
+    float *row = qkv + (size_t)t * ld;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t n_pairs = (n_head + n_kv) * half;
+    if (i < n_pairs) {
+        const uint32_t p = i % half;
+        float *v = row + 2 * (size_t)i;          // pairs of q, then of k (contiguous)
+        const float c = cos_tab[(size_t)pos * half + p], s = sin_tab[(size_t)pos * half + p];
+        const float v0 = v[0], v1 = v[1];
+        const float w0 = v0 * c - v1 * s, w1 = v0 * s + v1 * c;
+        if (i < n_head * half) {
+            v[0] = w0;
+            v[1] = w1;
+        } else {
+            const uint32_t e = 2 * (i - n_head * half);
+            kc[(size_t)pos * kvd + e] = w0;
+            kc[(size_t)pos * kvd + e + 1] = w1;
+        }
+    } else if (i < n_pairs + kvd / 2) {
+        const uint32_t e = 2 * (i - n_pairs);
+        const float *vv = row + (size_t)n_head * hd + kvd + e;
+        vc[(size_t)pos * kvd + e] = vv[0];
+        vc[(size_t)pos * kvd + e + 1] = vv[1];
+    }
+}
+
+hipError_t launch_rope_append(float *qkv, uint32_t ld, uint32_t n_tok, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                              uint32_t pos0, const float *cos_tab, const float *sin_tab, float *kc_layer,
+                              float *vc_layer, hipStream_t s)
+{
+    const uint32_t n = (n_head + n_kv) * (hd / 2) + n_kv * hd / 2;
+    hipLaunchKernelGGL(k_rope_append, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, ld, n_head, n_kv, hd, pos0,
+                       cos_tab, sin_tab, kc_layer, vc_layer);
+    return hipGetLastError();
+}
+
+// ── causal attention over the prompt ────────────────────────────────────────
+
+// Token t (position pos0 + t) and KV head h: the G query heads of the group
+// attend to cache rows 0..pos0+t (attention.c:142-164; softmax attention.c:18-33
+// as an online softmax in the log2 domain).  16 lanes hold one position (EPL =
+// hd/16 dimensions each), so a wave walks four positions at a time; the four
+// groups of a wave, then the four waves, merge their running (m, l, o).
+template <int EPL, int G>
+__global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ qkv, uint32_t ld,
+                                                      const float *__restrict__ kc, const float *__restrict__ vc,
+                                                      float *__restrict__ out, uint32_t n_kv, uint32_t pos0)
+{
+    constexpr int HD = 16 * EPL, NW = 4;
+    __shared__ float s_o[NW][G][HD];
+    __shared__ float s_m[NW][G], s_l[NW][G];
+    const uint32_t t = blockIdx.x, h = blockIdx.y, n_pos = pos0 + t + 1, kvd = n_kv * HD;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, l16 = lane & 15;
+    const float sc = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;      // attention.c:143, log2 units
+    const float *q = qkv + (size_t)t * ld + (size_t)h * G * HD;
+    float qv[G][EPL], m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            qv[g][e] = q[g * HD + l16 * EPL + e];
+            o[g][e] = 0.f;
+        }
+    }
+    for (uint32_t p = wave * 4 + grp; p < n_pos; p += 4 * NW) {
+        const float *kr = kc + (size_t)p * kvd + h * HD + l16 * EPL;
+        const float *vr = vc + (size_t)p * kvd + h * HD + l16 * EPL;
+        float kk[EPL], vv[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) { kk[e] = kr[e]; vv[e] = vr[e]; }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qv[g][e], kk[e], d);
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) d += __shfl_xor(d, off, 16);
+            const float sg = d * sc, mx = fmaxf(m[g], sg);
+            const float c = exp2f(m[g] - mx), pe = exp2f(sg - mx);
+            l[g] = l[g] * c + pe;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(pe, vv[e], o[g][e] * c);
+            m[g] = mx;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {                          // the wave's four position groups
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+            const float mw = fmaxf(m[g], __shfl_xor(m[g], off, 64));
+            const float c = mw == -INFINITY ? 0.f : exp2f(m[g] - mw);
+            float lw = l[g] * c;
+            lw += __shfl_xor(lw, off, 64);
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                float ov = o[g][e] * c;
+                ov += __shfl_xor(ov, off, 64);
+                o[g][e] = ov;
+            }
+            m[g] = mw;
+            l[g] = lw;
+        }
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) s_o[wave][g][l16 * EPL + e] = o[g][e];
+            if (lane == 0) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * HD; i += 256) {       // merge the four waves
+        const int g = i / HD, d = i % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, s_m[w][g]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float c = M == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+            L = __builtin_fmaf(s_l[w][g], c, L);
+            O = __builtin_fmaf(s_o[w][g][d], c, O);
+        }
+        out[(size_t)t * (n_kv * G * HD) + ((size_t)h * G + g) * HD + d] = O / L;
+    }
+}
+
+template <int EPL>
+static hipError_t attn_prefill_g(uint32_t group, dim3 grid, hipStream_t s, const float *qkv, uint32_t ld,
+                                 const float *kc, const float *vc, float *out, uint32_t n_kv, uint32_t pos0)
+{
+    switch (group) {
+    case 1: hipLaunchKernelGGL((k_attn_prefill<EPL, 1>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
+    case 2: hipLaunchKernelGGL((k_attn_prefill<EPL, 2>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
+    case 4: hipLaunchKernelGGL((k_attn_prefill<EPL, 4>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
+    case 8: hipLaunchKernelGGL((k_attn_prefill<EPL, 8>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
+    default: return hipErrorNotSupported;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const float *qkv, uint32_t ld, uint32_t n_tok, const float *kc_layer,
+                               const float *vc_layer, float *out, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                               uint32_t pos0, hipStream_t s)
+{
+    if (!n_kv || n_head % n_kv) return hipErrorInvalidValue;
+    const dim3 grid(n_tok, n_kv);
+    const uint32_t g = n_head / n_kv;
+    switch (hd) {
+    case 32: return attn_prefill_g<2>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
+    case 48: return attn_prefill_g<3>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
+    case 64: return attn_prefill_g<4>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
+    case 128: return attn_prefill_g<8>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
+    default: return hipErrorNotSupported;
+    }
+}
+
+} // namespace fw

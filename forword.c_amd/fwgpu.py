@@ -154,6 +154,8 @@ def gpu_lib():
         _sig(L, "forword_gpu_generate_greedy", C.c_int, [vp, u32p, sz, sz, u32p])
         _sig(L, "forword_gpu_decode", C.c_int, [vp, sz, u32p])
         _sig(L, "forword_gpu_decode_from", C.c_int, [vp, u32, sz, sz, u32p])
+        _sig(L, "forword_gpu_prefill", fp, [vp, u32p, sz, sz])
+        _sig(L, "forword_gpu_prefill_argmax", C.c_int, [vp, u32p, sz, sz, u32p])
         _sig(L, "forword_gpu_ffn_swiglu", C.c_int, [vp, vp, sz, u32, vp, vp, sz, sz, vp])
         _sig(L, "forword_gpu_kv_write", C.c_int, [vp, sz, sz, sz, fp, fp])
         _sig(L, "forword_gpu_kv_read", C.c_int, [vp, sz, sz, sz, fp, fp])
@@ -348,6 +350,30 @@ class GpuModel:
         nxt = u32(0)
         _check(gpu_lib().forword_gpu_forward_argmax(self.h, token, pos, C.byref(nxt)), "forward_argmax")
         return nxt.value
+
+    def prefill(self, tokens, pos0: int = 0) -> np.ndarray:
+        """Batched forward of tokens at positions pos0..; logits of the last one."""
+        tk = np.ascontiguousarray(tokens, np.uint32)
+        p = gpu_lib().forword_gpu_prefill(self.h, tk.ctypes.data_as(u32p), tk.size, pos0)
+        if not p:
+            raise ForwordError(f"forword_gpu_prefill failed: {last_error()}")
+        return np.ctypeslib.as_array(p, shape=(self.n_vocab,)).copy()
+
+    def prefill_argmax(self, tokens, pos0: int = 0) -> int:
+        tk = np.ascontiguousarray(tokens, np.uint32)
+        nxt = u32(0)
+        _check(gpu_lib().forword_gpu_prefill_argmax(self.h, tk.ctypes.data_as(u32p), tk.size, pos0, C.byref(nxt)),
+               "prefill_argmax")
+        return nxt.value
+
+    def generate_greedy_batched(self, prompt, n_gen: int) -> np.ndarray:
+        """Greedy generation with the batched prefill: the prompt in one pass, then
+        the device-resident loop from the first generated token."""
+        first = self.prefill_argmax(prompt, 0)
+        if n_gen <= 1:
+            return np.array([first][:n_gen], np.uint32)
+        rest = self.decode_from(first, len(prompt), n_gen - 1)
+        return np.concatenate([[first], rest]).astype(np.uint32)
 
     def generate_greedy(self, prompt, n_gen: int) -> np.ndarray:
         pr = np.ascontiguousarray(prompt, np.uint32)

@@ -139,6 +139,23 @@ int forword_gpu_decode(forword_gpu_t *h, size_t n_steps, uint32_t *out_ids);
 int forword_gpu_decode_from(forword_gpu_t *h, uint32_t token, size_t pos, size_t n_steps, uint32_t *out_ids);
 
 /*
+ * Batched prompt forward: tokens[0..n_tokens) at positions pos0..pos0+n_tokens-1
+ * in one pass per layer (every weight matrix read once per 512 tokens, the
+ * linears as matrix-core GEMMs), writing their KV rows; returns the logits of
+ * the last token, owned by the handle as for forword_gpu_forward.  Replaces the
+ * token-by-token prefill loop main.c:145-151 (n_tokens transformer_forward
+ * calls, transformer.c:149-326) and is equal to it within the floating-point
+ * tolerance (the linears sum in another order).  NULL on invalid arguments
+ * (positions past max_ctx, token >= n_vocab) or a HIP error.  A greedy loop
+ * continues with forword_gpu_decode_from(h, argmax, pos0 + n_tokens, ...).
+ */
+float *forword_gpu_prefill(forword_gpu_t *h, const uint32_t *tokens, size_t n_tokens, size_t pos0);
+
+/* Same pass, only the greedy choice of the last token's logits comes back. */
+int forword_gpu_prefill_argmax(forword_gpu_t *h, const uint32_t *tokens, size_t n_tokens, size_t pos0,
+                               uint32_t *next);
+
+/*
  * Write / read rows of the device KV cache for one layer: positions
  * [pos0, pos0+n_pos), each row n_head_kv*head_dim floats, K post-RoPE
  * (kv_k/kv_v, kv_cache.h:45-51; the append in attention.c:135-140).
