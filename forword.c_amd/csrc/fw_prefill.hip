@@ -85,6 +85,140 @@ __global__ __launch_bounds__(PG_THREADS) void k_gemm_q(const float *__restrict__
             }
 }
 
+// Block b (0 or 1) of a dword-aligned block pair as 32 floats, each rounded
+// once as the reference dequantises it: d·(q − k) computed as fma(q, d, −k·d)
+// (exact product and k·d, one rounding), quant.c:258, quant_matvec.c:204-212.
+template <uint32_t T>
+__device__ __forceinline__ void deq_pair_block(const uint32_t *dw, int b, float (&w)[32])
+{
+    if constexpr (T == kQ4_0) {
+        const float d = h2f(b ? dw[4] >> 16 : dw[0]), m8 = -8.0f * d;
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = b ? dw[5 + k] : align16(dw[k + 1], dw[k]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                w[4 * k + e] = __builtin_fmaf((float)((lo >> (8 * e)) & 0xFFu), d, m8);
+                w[16 + 4 * k + e] = __builtin_fmaf((float)((hi >> (8 * e)) & 0xFFu), d, m8);
+            }
+        }
+    } else if constexpr (T == kQ5_0) {
+        const float d = h2f(b ? dw[5] >> 16 : dw[0]), m16 = -16.0f * d;
+        const uint32_t qh = b ? dw[6] : align16(dw[1], dw[0]);
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = b ? dw[7 + k] : align16(dw[k + 2], dw[k + 1]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 4 * k + e;
+                const uint32_t ql = ((lo >> (8 * e)) & 0xFFu) | (((qh >> j) & 1u) << 4);
+                const uint32_t qu = ((hi >> (8 * e)) & 0xFFu) | (((qh >> (j + 16)) & 1u) << 4);
+                w[j] = __builtin_fmaf((float)ql, d, m16);
+                w[16 + j] = __builtin_fmaf((float)qu, d, m16);
+            }
+        }
+    } else {
+        const float d = h2f(b ? dw[8] >> 16 : dw[0]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t v = b ? dw[9 + k] : align16(dw[k + 1], dw[k]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[4 * k + e] = d * (float)((int32_t)(v << (24 - 8 * e)) >> 24);
+        }
+    }
+}
+
+// The same tile with K in block pairs (64 columns): the input tile moves as
+// float4, each thread dequantises one block of a weight row from dword loads,
+// and the next pair's loads are in flight while the matrix cores work on the
+// current one.  Needs n_in % 64 == 0 (so rows are dword aligned).
+constexpr int PP_BK = 64, PP_XS = PP_BK + 4;
+
+template <uint32_t T>
+__global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict__ X, uint32_t ldx,
+                                                        const uint8_t *__restrict__ W, uint64_t row_bytes,
+                                                        float *__restrict__ Y, uint32_t ldy, uint32_t n_tok,
+                                                        uint32_t n_out, uint32_t n_in, int accumulate)
+{
+    constexpr int PDW = Blk<T>::pair_dw, XV = PG_BM * PP_BK / 4 / PG_THREADS;   // float4 of x per thread
+    __shared__ __align__(16) float Xs[PG_BM][PP_XS];
+    __shared__ __align__(16) float Ws[PG_BN][PP_XS];
+    const uint32_t r0 = blockIdx.x * PG_BN, t0 = blockIdx.y * PG_BM;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    floatx4 acc[2][4];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 4; ni++) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int wr = tid >> 1, wb = tid & 1;                 // weight row of the tile, block of the pair
+    const uint32_t r = r0 + wr;
+    const uint8_t *wrow = W + (size_t)min(r, n_out - 1) * row_bytes;
+    float4 xr[XV];
+    uint32_t wd[PDW];
+    auto fetch = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const int e = tid + i * PG_THREADS, m = e / (PP_BK / 4), c4 = e % (PP_BK / 4);
+            const uint32_t t = t0 + m;
+            xr[i] = t < n_tok ? *reinterpret_cast<const float4 *>(X + (size_t)t * ldx + k0 + 4 * c4)
+                              : float4{0.f, 0.f, 0.f, 0.f};
+        }
+        load_pair<T>(wrow + (size_t)(k0 / 64) * (2 * Blk<T>::bytes), wd);
+    };
+    fetch(0);
+    for (uint32_t k0 = 0; k0 < n_in; k0 += PP_BK) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const int e = tid + i * PG_THREADS, m = e / (PP_BK / 4), c4 = e % (PP_BK / 4);
+            *reinterpret_cast<float4 *>(&Xs[m][4 * c4]) = xr[i];
+        }
+        {
+            float w[32];
+            deq_pair_block<T>(wd, wb, w);
+#pragma unroll
+            for (int j = 0; j < 32; j += 4)
+                *reinterpret_cast<float4 *>(&Ws[wr][32 * wb + j]) =
+                    r < n_out ? float4{w[j], w[j + 1], w[j + 2], w[j + 3]} : float4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+        if (k0 + PP_BK < n_in) fetch(k0 + PP_BK);
+#pragma unroll
+        for (int kk = 0; kk < PP_BK; kk += 4) {
+            float a[2], b[4];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) a[mi] = Xs[wm * 32 + mi * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+            for (int ni = 0; ni < 4; ni++) b[ni] = Ws[wn * 64 + ni * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int ni = 0; ni < 4; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 4; ni++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t t = t0 + wm * 32 + mi * 16 + 4 * (lane >> 4) + i;
+                const uint32_t rr = r0 + wn * 64 + ni * 16 + (lane & 15);
+                if (t < n_tok && rr < n_out) {
+                    float *p = Y + (size_t)t * ldy + rr;
+                    *p = accumulate ? *p + acc[mi][ni][i] : acc[mi][ni][i];
+                }
+            }
+}
+
 hipError_t launch_gemm_q(uint32_t type, const float *x, uint32_t ldx, const uint8_t *w, uint64_t row_bytes, float *y,
                          uint32_t ldy, uint32_t n_tok, uint32_t n_out, uint32_t n_in, bool accumulate,
                          hipStream_t s)
@@ -92,12 +226,16 @@ hipError_t launch_gemm_q(uint32_t type, const float *x, uint32_t ldx, const uint
     if (!n_tok || !n_out || !n_in || n_in % 32) return hipErrorInvalidValue;
     const dim3 grid((n_out + PG_BN - 1) / PG_BN, (n_tok + PG_BM - 1) / PG_BM);
     const int acc = accumulate ? 1 : 0;
+    // block pairs when rows are whole pairs at dword-aligned addresses and x rows float4 aligned
+    const bool pairs = n_in % 64 == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
+#define GEMM(K, TY) hipLaunchKernelGGL(K<TY>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc)
     switch (type) {
-    case kQ4_0: hipLaunchKernelGGL(k_gemm_q<kQ4_0>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc); break;
-    case kQ5_0: hipLaunchKernelGGL(k_gemm_q<kQ5_0>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc); break;
-    case kQ8_0: hipLaunchKernelGGL(k_gemm_q<kQ8_0>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc); break;
+    case kQ4_0: if (pairs) GEMM(k_gemm_qp, kQ4_0); else GEMM(k_gemm_q, kQ4_0); break;
+    case kQ5_0: if (pairs) GEMM(k_gemm_qp, kQ5_0); else GEMM(k_gemm_q, kQ5_0); break;
+    case kQ8_0: if (pairs) GEMM(k_gemm_qp, kQ8_0); else GEMM(k_gemm_q, kQ8_0); break;
     default: return hipErrorNotSupported;
     }
+#undef GEMM
     return hipGetLastError();
 }
 
