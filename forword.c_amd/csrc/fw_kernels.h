@@ -97,6 +97,16 @@ hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);
 
 // Batched prompt forward (fw_prefill.hip).
+// Up to three weight matrices of one type and column count computed as one
+// output of end[n_seg-1] rows: matrix i gives rows end[i-1] .. end[i]-1.
+struct GemmW {
+    const uint8_t *w[3];
+    uint64_t rb[3];
+    uint32_t end[3];
+    uint32_t n_seg;
+};
+hipError_t launch_gemm_qs(uint32_t type, const float *x, uint32_t ldx, const GemmW &g, float *y, uint32_t ldy,
+                          uint32_t n_tok, uint32_t n_in, bool accumulate, hipStream_t s);
 // Y[t][r] (+)= Σ_k X[t][k]·W[r][k] for t < n_tok, r < n_out: X fp32 rows ldx
 // apart, W Q4_0/Q5_0/Q8_0 rows of n_in columns, Y rows ldy apart.
 hipError_t launch_gemm_q(uint32_t type, const float *x, uint32_t ldx, const uint8_t *w, uint64_t row_bytes, float *y,

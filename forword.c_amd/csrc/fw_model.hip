@@ -719,9 +719,18 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
             const Layer &Ly = h->L[l];
             float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
             TRY(launch_rmsnorm_rows(X, Ly.attn_norm, Xn, n, rows, c.norm_eps, s));            // transformer.c:255
-            TRY(launch_gemm_q(Ly.q.type, Xn, n, Ly.q.w, Ly.q.row_bytes, QKV, ldqkv, rows, nq, n, false, s));
-            TRY(launch_gemm_q(Ly.k.type, Xn, n, Ly.k.w, Ly.k.row_bytes, QKV + nq, ldqkv, rows, kvd, n, false, s));
-            TRY(launch_gemm_q(Ly.v.type, Xn, n, Ly.v.w, Ly.v.row_bytes, QKV + nq + kvd, ldqkv, rows, kvd, n, false, s));
+            if (Ly.q.type == Ly.k.type && Ly.k.type == Ly.v.type) {                           // q | k | v rows
+                GemmW g{};
+                g.w[0] = Ly.q.w; g.w[1] = Ly.k.w; g.w[2] = Ly.v.w;
+                g.rb[0] = Ly.q.row_bytes; g.rb[1] = Ly.k.row_bytes; g.rb[2] = Ly.v.row_bytes;
+                g.end[0] = nq; g.end[1] = nq + kvd; g.end[2] = nq + 2 * kvd; g.n_seg = 3;
+                TRY(launch_gemm_qs(Ly.q.type, Xn, n, g, QKV, ldqkv, rows, n, false, s));
+            } else {
+                TRY(launch_gemm_q(Ly.q.type, Xn, n, Ly.q.w, Ly.q.row_bytes, QKV, ldqkv, rows, nq, n, false, s));
+                TRY(launch_gemm_q(Ly.k.type, Xn, n, Ly.k.w, Ly.k.row_bytes, QKV + nq, ldqkv, rows, kvd, n, false, s));
+                TRY(launch_gemm_q(Ly.v.type, Xn, n, Ly.v.w, Ly.v.row_bytes, QKV + nq + kvd, ldqkv, rows, kvd, n, false,
+                                  s));
+            }
             TRY(launch_rope_append(QKV, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
             TRY(launch_attn_prefill(QKV, ldqkv, rows, kc, vc, Att, c.n_head, c.n_head_kv, hd, p0, s));
             TRY(launch_gemm_q(Ly.o.type, Att, nq, Ly.o.w, Ly.o.row_bytes, X, n, rows, n, nq, true, s));   // :271-272

@@ -141,10 +141,9 @@ __device__ __forceinline__ void deq_pair_block(const uint32_t *dw, int b, float 
 constexpr int PP_BK = 64, PP_XS = PP_BK + 4;
 
 template <uint32_t T>
-__global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict__ X, uint32_t ldx,
-                                                        const uint8_t *__restrict__ W, uint64_t row_bytes,
+__global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict__ X, uint32_t ldx, GemmW g,
                                                         float *__restrict__ Y, uint32_t ldy, uint32_t n_tok,
-                                                        uint32_t n_out, uint32_t n_in, int accumulate)
+                                                        uint32_t n_in, int accumulate)
 {
     constexpr int PDW = Blk<T>::pair_dw, XV = PG_BM * PP_BK / 4 / PG_THREADS;   // float4 of x per thread
     __shared__ __align__(16) float Xs[PG_BM][PP_XS];
@@ -157,9 +156,18 @@ __global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict_
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
         for (int ni = 0; ni < 4; ni++) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // the matrix this tile's rows belong to (segments end on tile boundaries)
+    const uint32_t n_out = g.end[g.n_seg - 1];
+    const uint8_t *W = g.w[0];
+    uint64_t row_bytes = g.rb[0];
+    uint32_t base = 0;
+    if (g.n_seg > 1 && r0 >= g.end[0]) {
+        W = g.w[1]; row_bytes = g.rb[1]; base = g.end[0];
+        if (g.n_seg > 2 && r0 >= g.end[1]) { W = g.w[2]; row_bytes = g.rb[2]; base = g.end[1]; }
+    }
     const int wr = tid >> 1, wb = tid & 1;                 // weight row of the tile, block of the pair
     const uint32_t r = r0 + wr;
-    const uint8_t *wrow = W + (size_t)min(r, n_out - 1) * row_bytes;
+    const uint8_t *wrow = W + (size_t)(min(r, n_out - 1) - base) * row_bytes;
     float4 xr[XV];
     uint32_t wd[PDW];
     auto fetch = [&](uint32_t k0) {
@@ -223,20 +231,53 @@ hipError_t launch_gemm_q(uint32_t type, const float *x, uint32_t ldx, const uint
                          uint32_t ldy, uint32_t n_tok, uint32_t n_out, uint32_t n_in, bool accumulate,
                          hipStream_t s)
 {
-    if (!n_tok || !n_out || !n_in || n_in % 32) return hipErrorInvalidValue;
-    const dim3 grid((n_out + PG_BN - 1) / PG_BN, (n_tok + PG_BM - 1) / PG_BM);
+    GemmW g{};
+    g.w[0] = w; g.rb[0] = row_bytes; g.end[0] = n_out; g.n_seg = 1;
+    return launch_gemm_qs(type, x, ldx, g, y, ldy, n_tok, n_in, accumulate, s);
+}
+
+hipError_t launch_gemm_qs(uint32_t type, const float *x, uint32_t ldx, const GemmW &g, float *y, uint32_t ldy,
+                          uint32_t n_tok, uint32_t n_in, bool accumulate, hipStream_t s)
+{
+    if (!n_tok || !n_in || n_in % 32 || g.n_seg < 1 || g.n_seg > 3) return hipErrorInvalidValue;
+    const uint32_t n_out = g.end[g.n_seg - 1];
+    if (!n_out) return hipErrorInvalidValue;
     const int acc = accumulate ? 1 : 0;
-    // block pairs when rows are whole pairs at dword-aligned addresses and x rows float4 aligned
-    const bool pairs = n_in % 64 == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
-#define GEMM(K, TY) hipLaunchKernelGGL(K<TY>, grid, dim3(PG_THREADS), 0, s, x, ldx, w, row_bytes, y, ldy, n_tok, n_out, n_in, acc)
-    switch (type) {
-    case kQ4_0: if (pairs) GEMM(k_gemm_qp, kQ4_0); else GEMM(k_gemm_q, kQ4_0); break;
-    case kQ5_0: if (pairs) GEMM(k_gemm_qp, kQ5_0); else GEMM(k_gemm_q, kQ5_0); break;
-    case kQ8_0: if (pairs) GEMM(k_gemm_qp, kQ8_0); else GEMM(k_gemm_q, kQ8_0); break;
-    default: return hipErrorNotSupported;
+    // block pairs when rows are whole pairs at dword-aligned addresses, x rows float4 aligned and
+    // every matrix starts on a tile boundary; else one launch of the general kernel per matrix
+    bool pairs = n_in % 64 == 0 && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
+    for (uint32_t i = 0; i < g.n_seg; i++) {
+        pairs = pairs && ((uintptr_t)g.w[i] & 3) == 0;
+        if (i + 1 < g.n_seg) pairs = pairs && g.end[i] % PG_BN == 0;
     }
+    if (pairs) {
+        const dim3 grid((n_out + PG_BN - 1) / PG_BN, (n_tok + PG_BM - 1) / PG_BM);
+#define GEMM(TY) hipLaunchKernelGGL(k_gemm_qp<TY>, grid, dim3(PG_THREADS), 0, s, x, ldx, g, y, ldy, n_tok, n_in, acc)
+        switch (type) {
+        case kQ4_0: GEMM(kQ4_0); break;
+        case kQ5_0: GEMM(kQ5_0); break;
+        case kQ8_0: GEMM(kQ8_0); break;
+        default: return hipErrorNotSupported;
+        }
 #undef GEMM
-    return hipGetLastError();
+        return hipGetLastError();
+    }
+    for (uint32_t i = 0; i < g.n_seg; i++) {
+        const uint32_t r0 = i ? g.end[i - 1] : 0u, rows = g.end[i] - r0;
+        const dim3 grid((rows + PG_BN - 1) / PG_BN, (n_tok + PG_BM - 1) / PG_BM);
+        float *yo = y + r0;
+#define GEMM(TY) hipLaunchKernelGGL(k_gemm_q<TY>, grid, dim3(PG_THREADS), 0, s, x, ldx, g.w[i], g.rb[i], yo, ldy, n_tok, rows, n_in, acc)
+        switch (type) {
+        case kQ4_0: GEMM(kQ4_0); break;
+        case kQ5_0: GEMM(kQ5_0); break;
+        case kQ8_0: GEMM(kQ8_0); break;
+        default: return hipErrorNotSupported;
+        }
+#undef GEMM
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // ── embedding rows, RMSNorm rows ────────────────────────────────────────────
