@@ -200,9 +200,49 @@ __device__ __forceinline__ float dot_single(const uint8_t *p, const float *x, fl
     }
 }
 
-// Element j (0..31) of one block, exactly as the reference dequantises it.
+// 6-bit scale and min of group j of a Q4_K super-block (get_scale_min_k4, quant.c:66-85).
+__device__ __forceinline__ void scale_min_k4(uint32_t j, const uint8_t *q, uint32_t &sc, uint32_t &mn)
+{
+    if (j < 4) {
+        sc = q[j] & 63u;
+        mn = q[j + 4] & 63u;
+    } else {
+        sc = (q[j + 4] & 15u) | ((uint32_t)(q[j - 4] >> 6) << 4);
+        mn = (uint32_t)(q[j + 4] >> 4) | ((uint32_t)(q[j] >> 6) << 4);
+    }
+}
+
+// Value j (0..255) of a Q4_K super-block: (d*sc)*q - dmin*m, each product
+// rounded, then the difference (quant.c:111-126).
+__device__ __forceinline__ float dequant_q4_k(const uint8_t *blk, uint32_t j)
+{
+    const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    const float dmin = h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+    const uint32_t g = j / 32, i = j % 32;
+    uint32_t sc, mn;
+    scale_min_k4(g, blk + 4, sc, mn);
+    const uint8_t b = blk[16 + (g / 2) * 32 + i];
+    const float ds = d * (float)sc, dm = dmin * (float)mn;
+    return ds * (float)((g & 1) ? (b >> 4) : (b & 15)) - dm;
+}
+
+// Value j (0..255) of a Q6_K super-block: (d*sc)*(q-32) (quant.c:160-183).
+__device__ __forceinline__ float dequant_q6_k(const uint8_t *blk, uint32_t j)
+{
+    const uint32_t h = j / 128, r = j % 128, k = r / 32, l = r % 32;
+    const uint8_t a = blk[h * 64 + l + 32 * (k & 1)], hb = blk[128 + h * 32 + l];
+    const int q = (int)(((k >= 2) ? (a >> 4) : (a & 15)) | (((hb >> (2 * k)) & 3) << 4));
+    const int8_t sc = (int8_t)blk[192 + h * 8 + l / 16 + 2 * k];
+    const float d = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+    return (d * (float)sc) * (float)(q - 32);
+}
+
+// Element j of one block (0..31; 0..255 for the K super-blocks), exactly as the
+// reference dequantises it.
 __device__ __forceinline__ float dequant_one(const uint8_t *blk, uint32_t type, uint32_t j)
 {
+    if (type == kQ4_K) return dequant_q4_k(blk, j);
+    if (type == kQ6_K) return dequant_q6_k(blk, j);
     float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
     if (type == kQ8_0) return d * (float)(int8_t)blk[2 + j];                    // quant.c:258
     if (type == kQ4_0) {
@@ -219,7 +259,12 @@ __device__ __forceinline__ float dequant_one(const uint8_t *blk, uint32_t type, 
 
 __device__ __forceinline__ uint32_t block_bytes_dev(uint32_t t)
 {
-    return t == kQ4_0 ? 18u : t == kQ5_0 ? 22u : 34u;
+    return t == kQ4_0 ? 18u : t == kQ5_0 ? 22u : t == kQ4_K ? 144u : t == kQ6_K ? 210u : 34u;
+}
+
+__device__ __forceinline__ uint32_t block_values_dev(uint32_t t)
+{
+    return t == kQ4_K || t == kQ6_K ? 256u : 32u;
 }
 
 // Sum over the 64 lanes of a wave; every lane receives the total.

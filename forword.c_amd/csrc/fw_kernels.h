@@ -8,7 +8,7 @@
 namespace fw {
 
 // ggml type ids on the path (gguf.c:155-174)
-enum : uint32_t { kF32 = 0, kQ4_0 = 2, kQ5_0 = 6, kQ8_0 = 8 };
+enum : uint32_t { kF32 = 0, kQ4_0 = 2, kQ5_0 = 6, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
 
 // Device-resident step state read by every kernel of a token step, so one
 // captured graph serves every position.

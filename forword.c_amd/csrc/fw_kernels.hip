@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
             for (int k = 0; k < R; k++)
                 if (ok[k]) acc[k] = __builtin_fmaf(reinterpret_cast<const float *>(wr[k])[c], xc, acc[k]);
         }
-    } else if constexpr (PAIR) {
+    } else if constexpr (PAIR && T != kQ4_K && T != kQ6_K) {
         constexpr int BB = Blk<T>::bytes, NDW = Blk<T>::pair_dw;
         const uint32_t n_pairs = a.n_cols / 64;
         for (uint32_t p = lane; p < n_pairs; p += 64) {
@@ -151,6 +151,47 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
 #pragma unroll
             for (int k = 0; k < R; k++)
                 if (ok[k]) acc[k] += dot_pair<T>(dw[k], xv, sx0, sx1);
+        }
+    } else if constexpr (T == kQ4_K || T == kQ6_K) {
+        // 32-value groups of the 256-value super-blocks, one per lane at a time:
+        // the group's values exactly as the reference decodes them, then FMAs.
+        constexpr uint32_t SB = T == kQ4_K ? 144u : 210u;
+        const uint32_t n_units = a.n_cols / 32;
+        for (uint32_t u = lane; u < n_units; u += 64) {
+            float xv[32];
+            load_input<32>(a, 32 * (size_t)u, xv, xv4, nscale);
+            const uint32_t sb = u / 8, g = u % 8;
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+                if (!ok[k]) continue;
+                const uint8_t *blk = wr[k] + (size_t)sb * SB;
+                float s = 0.f;
+                if constexpr (T == kQ4_K) {
+                    const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+                    const float dmin = h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+                    uint32_t sc, mn;
+                    scale_min_k4(g, blk + 4, sc, mn);
+                    const float ds = d * (float)sc, dm = dmin * (float)mn;
+                    const uint8_t *q = blk + 16 + (g / 2) * 32;
+#pragma unroll
+                    for (int i = 0; i < 32; i++) {
+                        const uint32_t v = (g & 1) ? (uint32_t)(q[i] >> 4) : (uint32_t)(q[i] & 15);
+                        s = __builtin_fmaf(ds * (float)v - dm, xv[i], s);
+                    }
+                } else {
+                    const uint32_t h = g / 4, kk = g % 4;
+                    const uint8_t *ql = blk + h * 64 + 32 * (kk & 1), *qh = blk + 128 + h * 32;
+                    const float d = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+                    const float s0 = d * (float)(int8_t)blk[192 + h * 8 + 2 * kk];
+                    const float s1 = d * (float)(int8_t)blk[192 + h * 8 + 2 * kk + 1];
+#pragma unroll
+                    for (int l = 0; l < 32; l++) {
+                        const int q = (int)(((kk >= 2) ? (ql[l] >> 4) : (ql[l] & 15)) | (((qh[l] >> (2 * kk)) & 3) << 4));
+                        s = __builtin_fmaf((l < 16 ? s0 : s1) * (float)(q - 32), xv[l], s);
+                    }
+                }
+                acc[k] += s;
+            }
         }
     } else {
         constexpr int BB = Blk<T>::bytes;
@@ -241,7 +282,7 @@ void qmv_plan(QmvArgs &a, int epi)
 
 bool qmv_pair_ok(uint32_t type, uint32_t n_cols, const void *base)
 {
-    return type != kF32 && n_cols % 64 == 0 && ((uintptr_t)base & 3) == 0;
+    return (type == kQ4_0 || type == kQ5_0 || type == kQ8_0) && n_cols % 64 == 0 && ((uintptr_t)base & 3) == 0;
 }
 
 template <uint32_t T, int EPI>
@@ -263,6 +304,8 @@ static hipError_t launch_e(uint32_t type, const QmvArgs &a, hipStream_t s)
     case kQ4_0: return launch_t<kQ4_0, EPI>(a, pair, s);
     case kQ5_0: return launch_t<kQ5_0, EPI>(a, pair, s);
     case kQ8_0: return launch_t<kQ8_0, EPI>(a, pair, s);
+    case kQ4_K: return launch_t<kQ4_K, EPI>(a, false, s);
+    case kQ6_K: return launch_t<kQ6_K, EPI>(a, false, s);
     case kF32: return launch_t<kF32, EPI>(a, false, s);
     default: return hipErrorInvalidValue;
     }
@@ -364,9 +407,9 @@ __global__ __launch_bounds__(1024) void k_row(const uint8_t *w, uint32_t type, u
         float v;
         if (type == kF32) v = reinterpret_cast<const float *>(w)[(size_t)row * n_cols + j];
         else {
-            uint32_t bb = block_bytes_dev(type);
-            const uint8_t *blk = w + (size_t)row * (n_cols / 32) * bb + (size_t)(j / 32) * bb;
-            v = dequant_one(blk, type, j & 31);
+            const uint32_t bb = block_bytes_dev(type), bv = block_values_dev(type);
+            const uint8_t *blk = w + (size_t)row * (n_cols / bv) * bb + (size_t)(j / bv) * bb;
+            v = dequant_one(blk, type, j % bv);
         }
         if (embd_scale != 1.0f) v *= embd_scale;               // transformer.c:179-182
         out[j] = v;
@@ -398,15 +441,15 @@ hipError_t launch_get_row(const uint8_t *w, uint32_t type, uint32_t n_cols, uint
 
 __global__ void k_dequant(const uint8_t *blocks, uint32_t type, uint64_t n, float *out)
 {
-    uint32_t bb = block_bytes_dev(type);
+    const uint32_t bb = block_bytes_dev(type), bv = block_values_dev(type);
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x)
-        out[i] = dequant_one(blocks + (i / 32) * bb, type, (uint32_t)(i & 31));
+        out[i] = dequant_one(blocks + (i / bv) * bb, type, (uint32_t)(i % bv));
 }
 
 hipError_t launch_dequant(const uint8_t *blocks, uint32_t type, uint64_t n_blocks, float *out, hipStream_t s)
 {
-    uint64_t n = n_blocks * 32;
+    uint64_t n = n_blocks * (type == kQ4_K || type == kQ6_K ? 256u : 32u);
     uint64_t g = (n + 255) / 256;
     if (g > 65536) g = 65536;
     hipLaunchKernelGGL(k_dequant, dim3((uint32_t)g), dim3(256), 0, s, blocks, type, n, out);

@@ -71,6 +71,19 @@ uint64_t type_row_bytes(uint32_t type, uint64_t cols)
     case kQ4_0: return cols / 32 * 18;
     case kQ5_0: return cols / 32 * 22;
     case kQ8_0: return cols / 32 * 34;
+    case kQ4_K: return cols / 256 * 144;
+    case kQ6_K: return cols / 256 * 210;
+    default: return 0;
+    }
+}
+
+// Values per block of a block type (gguf.c:211-223); 1 for F32, 0 unknown.
+uint32_t type_block_values(uint32_t type)
+{
+    switch (type) {
+    case kF32: return 1;
+    case kQ4_0: case kQ5_0: case kQ8_0: return 32;
+    case kQ4_K: case kQ6_K: return 256;
     default: return 0;
     }
 }
@@ -139,7 +152,7 @@ static int bind_lin(forword_gpu_t *h, Lin &l, const forword_gpu_tensor_t *t, con
                     uint64_t out)
 {
     if (!t) { set_err("missing tensor %s", name); return -1; }
-    if (t->ggml_type != kF32 && t->ggml_type != kQ4_0 && t->ggml_type != kQ5_0 && t->ggml_type != kQ8_0) {
+    if (!type_block_values(t->ggml_type)) {
         set_err("tensor %s: unsupported ggml type %u", name, t->ggml_type);
         return -1;
     }
@@ -149,7 +162,10 @@ static int bind_lin(forword_gpu_t *h, Lin &l, const forword_gpu_tensor_t *t, con
                 (unsigned long long)out);
         return -1;
     }
-    if (t->ggml_type != kF32 && in % 32) { set_err("tensor %s: columns not a multiple of 32", name); return -1; }
+    if (in % type_block_values(t->ggml_type)) {
+        set_err("tensor %s: columns not a multiple of the %u-value block", name, type_block_values(t->ggml_type));
+        return -1;
+    }
     uint64_t rb = type_row_bytes(t->ggml_type, in);
     if (in >= (1u << 31) || out >= (1u << 31) || t->offset > h->data_size ||
         rb * out > h->data_size - t->offset) {
@@ -677,7 +693,7 @@ extern "C" int forword_gpu_decode_from(forword_gpu_t *h, uint32_t token, size_t 
 // attending to the cache rows the previous ones wrote.
 static constexpr uint32_t kPrefillChunk = 512;
 
-static bool prefill_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
+static bool prefill_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
 
 // Queue the batched forward of tokens[0..n_tok) at positions pos0.. (KV rows
 // written), the last token's logits into d_logits and their argmax into d_argmax.
@@ -894,8 +910,8 @@ extern "C" int forword_gpu_quant_matvec(const void *weights, size_t weights_size
     if (!weights || !input || !output || !in || !out) { set_err("quant_matvec: invalid arguments"); return -1; }
     uint64_t rb;
     if (type == kF32) rb = (uint64_t)in * 4;
-    else if (type == kQ4_0 || type == kQ5_0 || type == kQ8_0) {
-        if (in % 32) { set_err("quant_matvec: input size not a multiple of 32"); return -1; }
+    else if (type_block_values(type)) {
+        if (in % type_block_values(type)) { set_err("quant_matvec: input size not a multiple of the block size"); return -1; }
         rb = type_row_bytes(type, in);
     } else { set_err("quant_matvec: unsupported ggml type %u", type); return -1; }
     if (in >= (1u << 31) || out >= (1u << 31) || out > SIZE_MAX / rb || weights_size < out * rb) {
@@ -916,7 +932,7 @@ extern "C" int forword_gpu_ffn_swiglu(const void *w_gate, const void *w_up, size
                                       const float *x, float *hout, size_t in, size_t n_ff, void *stream)
 {
     if (!w_gate || !w_up || !x || !hout || !in || !n_ff) { set_err("ffn_swiglu: invalid arguments"); return -1; }
-    if ((type != kQ4_0 && type != kQ5_0 && type != kQ8_0 && type != kF32) || (type != kF32 && in % 32)) {
+    if (!type_block_values(type) || in % type_block_values(type)) {
         set_err("ffn_swiglu: unsupported type or input size");
         return -1;
     }
@@ -942,8 +958,9 @@ extern "C" int forword_gpu_tensor_matvec_f32(const float *weights, const float *
 extern "C" int forword_gpu_dequant(const void *blocks, size_t size, uint32_t type, float *out, size_t count,
                                    void *stream)
 {
-    uint64_t bb = type_row_bytes(type, 32);
-    if (!blocks || !out || type == kF32 || !bb || !size || size % bb || count % 32 || size / bb != count / 32) {
+    const uint32_t bv = type_block_values(type);
+    const uint64_t bb = bv ? type_row_bytes(type, bv) : 0;
+    if (!blocks || !out || type == kF32 || !bb || !size || size % bb || count % bv || size / bb != count / bv) {
         set_err("dequant: invalid arguments");
         return -1;
     }
@@ -954,7 +971,7 @@ extern "C" int forword_gpu_get_row(const void *w, size_t size, uint32_t type, si
                                    void *stream)
 {
     if (!w || !out || !n_cols || n_cols >= (1u << 31) || row >= (1u << 31)) { set_err("get_row: invalid arguments"); return -1; }
-    if (type != kF32 && (type_row_bytes(type, 32) == 0 || n_cols % 32)) { set_err("get_row: unsupported type or shape"); return -1; }
+    if (!type_block_values(type) || n_cols % type_block_values(type)) { set_err("get_row: unsupported type or shape"); return -1; }
     uint64_t rb = type_row_bytes(type, n_cols);
     if (rb == 0 || (row + 1) > size / rb) { set_err("get_row: row outside the tensor"); return -1; }
     return launched(launch_get_row((const uint8_t *)w, type, (uint32_t)n_cols, (uint32_t)row, out, (hipStream_t)stream),

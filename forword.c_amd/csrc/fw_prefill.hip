@@ -51,9 +51,13 @@ __global__ __launch_bounds__(PG_THREADS) void k_gemm_q(const float *__restrict__
             const uint32_t t = t0 + m;
             Xs[m][k] = t < n_tok ? X[(size_t)t * ldx + k0 + k] : 0.f;
         }
-        const uint8_t *blk = wrow + (size_t)(k0 / 32) * Blk<T>::bytes;
+        // K-quants: the 32 columns are one group of a 256-value super-block
+        constexpr uint32_t BV = T == kQ4_K || T == kQ6_K ? 256u : 32u;
+        constexpr uint32_t BBY = T == kQ4_K ? 144u : T == kQ6_K ? 210u : T == kQ4_0 ? 18u : T == kQ5_0 ? 22u : 34u;
+        const uint8_t *blk = wrow + (size_t)(k0 / BV) * BBY;
+        const uint32_t j0 = k0 % BV + 16 * wh;
 #pragma unroll
-        for (int j = 0; j < 16; j++) Ws[wr][16 * wh + j] = r < n_out ? dequant_one(blk, T, 16 * wh + j) : 0.f;
+        for (int j = 0; j < 16; j++) Ws[wr][16 * wh + j] = r < n_out ? dequant_one(blk, T, j0 + j) : 0.f;
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < PG_BK; kk += 4) {
@@ -245,7 +249,8 @@ hipError_t launch_gemm_qs(uint32_t type, const float *x, uint32_t ldx, const Gem
     const int acc = accumulate ? 1 : 0;
     // block pairs when rows are whole pairs at dword-aligned addresses, x rows float4 aligned and
     // every matrix starts on a tile boundary; else one launch of the general kernel per matrix
-    bool pairs = n_in % 64 == 0 && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
+    bool pairs = (type == kQ4_0 || type == kQ5_0 || type == kQ8_0) && n_in % 64 == 0 && ((uintptr_t)x & 15) == 0 &&
+                 ldx % 4 == 0;
     for (uint32_t i = 0; i < g.n_seg; i++) {
         pairs = pairs && ((uintptr_t)g.w[i] & 3) == 0;
         if (i + 1 < g.n_seg) pairs = pairs && g.end[i] % PG_BN == 0;
@@ -271,6 +276,8 @@ hipError_t launch_gemm_qs(uint32_t type, const float *x, uint32_t ldx, const Gem
         case kQ4_0: GEMM(kQ4_0); break;
         case kQ5_0: GEMM(kQ5_0); break;
         case kQ8_0: GEMM(kQ8_0); break;
+        case kQ4_K: GEMM(kQ4_K); break;
+        case kQ6_K: GEMM(kQ6_K); break;
         default: return hipErrorNotSupported;
         }
 #undef GEMM
@@ -293,8 +300,8 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint8_t *w, uint32_t t
     float v;
     if (type == kF32) v = reinterpret_cast<const float *>(w)[(size_t)tok * n_cols + j];
     else {
-        const uint32_t bb = block_bytes_dev(type);
-        v = dequant_one(w + (size_t)tok * (n_cols / 32) * bb + (size_t)(j / 32) * bb, type, j & 31);
+        const uint32_t bb = block_bytes_dev(type), bv = block_values_dev(type);
+        v = dequant_one(w + (size_t)tok * (n_cols / bv) * bb + (size_t)(j / bv) * bb, type, j % bv);
     }
     if (embd_scale != 1.0f) v *= embd_scale;
     X[(size_t)t * n_cols + j] = v;

@@ -27,9 +27,11 @@ LIBDIR = os.path.join(HERE, "lib")
 HOST_LIB = os.path.join(LIBDIR, "libfw_host.so")
 GPU_LIB = os.path.join(LIBDIR, "libforword_gpu.so")
 
-GGML_F32, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0 = 0, 2, 6, 8
-BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q5_0: 22, GGML_Q8_0: 34}
-TYPE_NAMES = {GGML_F32: "F32", GGML_Q4_0: "Q4_0", GGML_Q5_0: "Q5_0", GGML_Q8_0: "Q8_0"}
+GGML_F32, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 2, 6, 8, 12, 14
+BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q5_0: 22, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
+BLOCK_VALUES = {GGML_Q4_0: 32, GGML_Q5_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
+TYPE_NAMES = {GGML_F32: "F32", GGML_Q4_0: "Q4_0", GGML_Q5_0: "Q5_0", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K",
+              GGML_Q6_K: "Q6_K"}
 
 u32, u64, i32, f32 = C.c_uint32, C.c_uint64, C.c_int32, C.c_float
 vp, sz = C.c_void_p, C.c_size_t
@@ -215,7 +217,7 @@ def randn(seed: int, n: int, std: float = 1.0) -> np.ndarray:
 def synth_matrix(ggml_type: int, rows: int, cols: int, seed: int, scale_std: float = 0.02,
                  subnormal_every: int = 0, threads: int = 0) -> np.ndarray:
     """Microbenchmark matrix of GGUF blocks (codes uniform, scales fp16(|N(0,1)|*scale_std))."""
-    n = rows * (cols // 32) * BLOCK_BYTES[ggml_type]
+    n = rows * (cols // BLOCK_VALUES[ggml_type]) * BLOCK_BYTES[ggml_type]
     out = np.empty(n, np.uint8)
     got = host_lib().fwh_synth_matrix(ggml_type, rows, cols, seed, scale_std, subnormal_every,
                                       out.ctypes.data, threads)
@@ -226,7 +228,7 @@ def synth_matrix(ggml_type: int, rows: int, cols: int, seed: int, scale_std: flo
 
 def quantize(ggml_type: int, x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
-    out = np.empty(x.size // 32 * BLOCK_BYTES[ggml_type], np.uint8)
+    out = np.empty(x.size // BLOCK_VALUES[ggml_type] * BLOCK_BYTES[ggml_type], np.uint8)
     if host_lib().fwh_quantize(ggml_type, x.ctypes.data_as(fp), x.size, out.ctypes.data) != out.size:
         raise ValueError("fwh_quantize failed")
     return out

@@ -12,6 +12,8 @@
  *   Q4_0 (18 B): fp16 d, qs[16]; w_j = d*((qs[j]&15)-8), w_{j+16} = d*((qs[j]>>4)-8)
  *   Q5_0 (22 B): fp16 d, qh u32 (LE), qs[16]; 5th bit of code j is bit j of qh
  *   Q8_0 (34 B): fp16 d, int8 qs[32]; w_j = d*qs[j]
+ *   Q4_K (144 B per 256): fp16 d, dmin, 12 B of 6-bit group scales/mins, qs[128]
+ *   Q6_K (210 B per 256): ql[128], qh[64], int8 scales[16], fp16 d
  * Quantisers follow ggml's reference rounding: Q8_0 d = amax/127 with
  * round-to-nearest codes; Q4_0/Q5_0 take the signed value of largest magnitude
  * m and use d = m/-8 (resp. m/-16), codes min(15, (int8)(x/d + 8.5)) (resp.
@@ -172,7 +174,19 @@ size_t fwh_block_bytes(uint32_t t)
     case FORWORD_GGML_Q4_0: return 18;
     case FORWORD_GGML_Q5_0: return 22;
     case FORWORD_GGML_Q8_0: return 34;
+    case FORWORD_GGML_Q4_K: return 144;
+    case FORWORD_GGML_Q6_K: return 210;
     case FORWORD_GGML_F32: return 4;
+    default: return 0;
+    }
+}
+
+size_t fwh_block_values(uint32_t t)
+{
+    switch (t) {
+    case FORWORD_GGML_Q4_0: case FORWORD_GGML_Q5_0: case FORWORD_GGML_Q8_0: return 32;
+    case FORWORD_GGML_Q4_K: case FORWORD_GGML_Q6_K: return 256;
+    case FORWORD_GGML_F32: return 1;
     default: return 0;
     }
 }
@@ -231,18 +245,100 @@ static void quant_q5_0(const float *x, uint8_t *b)
     b[2] = (uint8_t)qh; b[3] = (uint8_t)(qh >> 8); b[4] = (uint8_t)(qh >> 16); b[5] = (uint8_t)(qh >> 24);
 }
 
+/* Q4_K super-block (the layout q4_k_decode reads, quant.c:63-131): fp16 d and
+ * dmin, 12 bytes of 6-bit scale/min pairs per 32-value group, 128 code bytes
+ * (group 2k in the low nibbles of bytes 32k.., group 2k+1 in the high ones).
+ * Value = d*sc*q - dmin*m.  A simple encoder: per group the range above its
+ * minimum, both quantised against the super-block maxima. */
+static void quant_q4_k(const float *x, uint8_t *b)
+{
+    float scale[8], minv[8], smax = 0.0f, mmax = 0.0f;
+    for (int g = 0; g < 8; g++) {
+        float lo = x[32 * g], hi = x[32 * g];
+        for (int i = 1; i < 32; i++) { lo = fminf(lo, x[32 * g + i]); hi = fmaxf(hi, x[32 * g + i]); }
+        minv[g] = lo < 0.0f ? -lo : 0.0f;
+        scale[g] = (hi + minv[g]) / 15.0f;
+        smax = fmaxf(smax, scale[g]);
+        mmax = fmaxf(mmax, minv[g]);
+    }
+    const float d = smax / 63.0f, dmin = mmax / 63.0f;
+    put_f16(b, d);
+    put_f16(b + 2, dmin);
+    const float dq = fwh_f16_to_f32(fwh_f32_to_f16(d)), mq = fwh_f16_to_f32(fwh_f32_to_f16(dmin));
+    uint8_t sc[8], mn[8];
+    for (int g = 0; g < 8; g++) {
+        int s6 = dq > 0.0f ? (int)lroundf(scale[g] / dq) : 0, m6 = mq > 0.0f ? (int)lroundf(minv[g] / mq) : 0;
+        sc[g] = (uint8_t)(s6 < 0 ? 0 : s6 > 63 ? 63 : s6);
+        mn[g] = (uint8_t)(m6 < 0 ? 0 : m6 > 63 ? 63 : m6);
+    }
+    uint8_t *scales = b + 4;
+    for (int j = 0; j < 4; j++) {
+        scales[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        scales[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+        scales[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+    }
+    uint8_t *qs = b + 16;
+    memset(qs, 0, 128);
+    for (int g = 0; g < 8; g++) {
+        const float ds = dq * sc[g], dm = mq * mn[g];
+        for (int i = 0; i < 32; i++) {
+            int q = ds > 0.0f ? (int)lroundf((x[32 * g + i] + dm) / ds) : 0;
+            q = q < 0 ? 0 : q > 15 ? 15 : q;
+            qs[(g / 2) * 32 + i] |= (uint8_t)(g & 1 ? q << 4 : q);
+        }
+    }
+}
+
+/* Q6_K super-block (q6_k_decode, quant.c:133-188): ql[128] low nibbles, qh[64]
+ * high bit pairs, int8 scales[16] (one per 16 values), fp16 d.  Value =
+ * d*sc*(q - 32); within a half of 128 values, value l+32k (l < 32) has its low
+ * nibble in ql[l + 32(k&1)] (high nibble for k >= 2), its high bits in qh[l]
+ * bits 2k..2k+1, its scale in scales[l/16 + 2k]. */
+static void quant_q6_k(const float *x, uint8_t *b)
+{
+    float sub[16], smax = 0.0f;
+    for (int s = 0; s < 16; s++) {
+        float a = 0.0f;
+        for (int i = 0; i < 16; i++) a = fmaxf(a, fabsf(x[16 * s + i]));
+        sub[s] = a / 31.0f;
+        smax = fmaxf(smax, sub[s]);
+    }
+    const float d = smax / 127.0f;
+    put_f16(b + 208, d);
+    const float dq = fwh_f16_to_f32(fwh_f32_to_f16(d));
+    int8_t *sc = (int8_t *)(b + 192);
+    for (int s = 0; s < 16; s++) {
+        int v = dq > 0.0f ? (int)lroundf(sub[s] / dq) : 0;
+        sc[s] = (int8_t)(v > 127 ? 127 : v);
+    }
+    memset(b, 0, 192);
+    for (int h = 0; h < 2; h++)
+        for (int k = 0; k < 4; k++)
+            for (int l = 0; l < 32; l++) {
+                const int pos = h * 128 + 32 * k + l, s = h * 8 + l / 16 + 2 * k;
+                const float st = dq * sc[s];
+                int q = st > 0.0f ? (int)lroundf(x[pos] / st) + 32 : 32;
+                q = q < 0 ? 0 : q > 63 ? 63 : q;
+                uint8_t *ql = b + h * 64 + l + 32 * (k & 1), *qh = b + 128 + h * 32 + l;
+                *ql |= (uint8_t)(k >= 2 ? (q & 15) << 4 : (q & 15));
+                *qh |= (uint8_t)(((q >> 4) & 3) << (2 * k));
+            }
+}
+
 size_t fwh_quantize(uint32_t t, const float *src, size_t n, void *dst)
 {
     uint8_t *o = (uint8_t *)dst;
     if (t == FORWORD_GGML_F32) { memcpy(dst, src, n * 4); return n * 4; }
-    size_t bb = fwh_block_bytes(t);
-    if (!bb || n % 32) return 0;
-    for (size_t i = 0; i < n; i += 32, o += bb) {
+    const size_t bb = fwh_block_bytes(t), bv = fwh_block_values(t);
+    if (!bb || n % bv) return 0;
+    for (size_t i = 0; i < n; i += bv, o += bb) {
         if (t == FORWORD_GGML_Q8_0) quant_q8_0(src + i, o);
         else if (t == FORWORD_GGML_Q4_0) quant_q4_0(src + i, o);
-        else quant_q5_0(src + i, o);
+        else if (t == FORWORD_GGML_Q5_0) quant_q5_0(src + i, o);
+        else if (t == FORWORD_GGML_Q4_K) quant_q4_k(src + i, o);
+        else quant_q6_k(src + i, o);
     }
-    return (n / 32) * bb;
+    return (n / bv) * bb;
 }
 
 /* ── GGUF image writer ───────────────────────────────────────────────────── */
@@ -269,7 +365,7 @@ typedef struct {
 static uint64_t tbytes(uint32_t type, uint64_t cols, uint64_t rows)
 {
     if (type == FORWORD_GGML_F32) return cols * rows * 4;
-    return cols / 32 * fwh_block_bytes(type) * rows;
+    return cols / fwh_block_values(type) * fwh_block_bytes(type) * rows;
 }
 
 static void add_t(layout_t *L, const char *name, int kind, uint32_t type, uint64_t cols, uint64_t rows,
@@ -292,7 +388,9 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
     if (!s->n_embd || !s->n_layer || !s->n_head || !s->n_head_kv || !s->n_ff || !s->n_vocab ||
         s->n_embd % s->n_head || s->n_embd % 32 || s->n_ff % 32 || s->n_head % s->n_head_kv ||
         !fwh_block_bytes(s->linear_type) || !fwh_block_bytes(s->embd_type) ||
-        !fwh_block_bytes(s->output_type))
+        !fwh_block_bytes(s->output_type) || s->n_embd % fwh_block_values(s->linear_type) ||
+        s->n_ff % fwh_block_values(s->linear_type) || s->n_embd % fwh_block_values(s->embd_type) ||
+        s->n_embd % fwh_block_values(s->output_type))
         return -1;
     uint64_t hd = s->n_embd / s->n_head, kvd = hd * s->n_head_kv;
     L->t = (tdesc_t *)calloc(9 * (size_t)s->n_layer + 3, sizeof(tdesc_t));
@@ -496,12 +594,20 @@ static void mat_job(void *vctx, size_t r)
         size_t gb = r * c->blocks_per_row + b;
         if (c->subnormal_every && gb % c->subnormal_every == 0)
             h = (uint16_t)(1u + (fwh_splitmix64(&s) & 0x3feu));      /* subnormal, non-zero */
-        o[0] = (uint8_t)h;
-        o[1] = (uint8_t)(h >> 8);
-        for (size_t k = 2; k < c->bb; k += 8) {
+        const int kq = c->type == FORWORD_GGML_Q4_K || c->type == FORWORD_GGML_Q6_K;
+        for (size_t k = kq ? 0 : 2; k < c->bb; k += 8) {      /* 32-value blocks: codes after d */
             uint64_t v = fwh_splitmix64(&s);
             size_t n = c->bb - k < 8 ? c->bb - k : 8;
             memcpy(o + k, &v, n);
+        }
+        /* the fp16 scale fields: d at 0 (Q6_K: at 208), Q4_K's dmin at 2 */
+        const size_t d_at = c->type == FORWORD_GGML_Q6_K ? 208 : 0;
+        o[d_at] = (uint8_t)h;
+        o[d_at + 1] = (uint8_t)(h >> 8);
+        if (c->type == FORWORD_GGML_Q4_K) {
+            uint16_t hm = fwh_f32_to_f16(fabsf(z) * c->scale_std * 0.5f);
+            o[2] = (uint8_t)hm;
+            o[3] = (uint8_t)(hm >> 8);
         }
     }
 }
@@ -509,9 +615,9 @@ static void mat_job(void *vctx, size_t r)
 size_t fwh_synth_matrix(uint32_t type, size_t rows, size_t cols, uint64_t seed, float scale_std,
                         uint32_t subnormal_every, void *dst, uint32_t threads)
 {
-    size_t bb = fwh_block_bytes(type);
-    if (!dst || !bb || type == FORWORD_GGML_F32 || !rows || !cols || cols % 32) return 0;
-    mat_ctx_t c = { type, rows, cols, bb, cols / 32, seed, scale_std, subnormal_every, (uint8_t *)dst };
+    const size_t bb = fwh_block_bytes(type), bv = fwh_block_values(type);
+    if (!dst || !bb || type == FORWORD_GGML_F32 || !rows || !cols || cols % bv) return 0;
+    mat_ctx_t c = { type, rows, cols, bb, cols / bv, seed, scale_std, subnormal_every, (uint8_t *)dst };
     run_parallel(mat_job, &c, rows, threads);
-    return rows * (cols / 32) * bb;
+    return rows * (cols / bv) * bb;
 }

@@ -33,7 +33,9 @@ enum {
     FORWORD_GGML_F32  = 0,
     FORWORD_GGML_Q4_0 = 2,
     FORWORD_GGML_Q5_0 = 6,
-    FORWORD_GGML_Q8_0 = 8
+    FORWORD_GGML_Q8_0 = 8,
+    FORWORD_GGML_Q4_K = 12,   /* 256-value super-blocks (quant.c:63-189) */
+    FORWORD_GGML_Q6_K = 14
 };
 
 /* Architecture / variant enums, same numeric values as model_config.h:12-38. */

@@ -78,7 +78,9 @@ uint64_t fwh_splitmix64(uint64_t *state);
 void fwh_randn(uint64_t seed, float std, float *out, size_t n);
 
 /* ── Quantisers (GGUF/ggml block formats) ───────────────────────────────── */
-size_t fwh_block_bytes(uint32_t ggml_type);    /* 18/22/34 for Q4_0/Q5_0/Q8_0, 4 for F32, 0 unknown */
+size_t fwh_block_bytes(uint32_t ggml_type);    /* 18/22/34 for Q4_0/Q5_0/Q8_0, 144/210 for Q4_K/Q6_K,
+                                                  4 for F32, 0 unknown */
+size_t fwh_block_values(uint32_t ggml_type);   /* values per block: 32, 256 for Q4_K/Q6_K, 1 for F32 */
 /* Quantise n (multiple of 32) floats into dst; returns bytes written, 0 on error. */
 size_t fwh_quantize(uint32_t ggml_type, const float *src, size_t n, void *dst);
 

@@ -116,38 +116,103 @@ static void decode_q8_0(const uint8_t *p, float *w)
     for (int j = 0; j < 32; j++) w[j] = d * (float)qs[j];
 }
 
+/* get_scale_min_k4 (quant.c:66-85): 6-bit scale and min of group j. */
+static void scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *mn)
+{
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 15) | ((q[j - 4] >> 6) << 4));
+        *mn = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* q4_k_decode, one super-block (quant.c:87-131): y = (d*sc)*q - dmin*m, each
+ * product rounded, then the difference. */
+static void decode_q4_k(const uint8_t *p, float *y)
+{
+    const float d = fwc_half_to_float(rd16(p)), dmin = fwc_half_to_float(rd16(p + 2));
+    const uint8_t *scales = p + 4, *qs = p + 16;
+    for (int g = 0; g < 8; g++) {
+        uint8_t sc, mn;
+        scale_min_k4(g, scales, &sc, &mn);
+        const float ds = d * sc, dm = dmin * mn;
+        const uint8_t *q = qs + (g / 2) * 32;
+        for (int i = 0; i < 32; i++) {
+            const uint8_t v = (g & 1) ? (uint8_t)(q[i] >> 4) : (uint8_t)(q[i] & 15);
+            y[g * 32 + i] = ds * v - dm;
+        }
+    }
+}
+
+/* q6_k_decode, one super-block (quant.c:133-188): y = (d*sc)*(q-32). */
+static void decode_q6_k(const uint8_t *p, float *y)
+{
+    const uint8_t *ql = p, *qh = p + 128;
+    const int8_t *sc = (const int8_t *)(p + 192);
+    const float d = fwc_half_to_float(rd16(p + 208));
+    for (int h = 0; h < 2; h++) {
+        const uint8_t *a = ql + h * 64, *hb = qh + h * 32;
+        const int8_t *s = sc + h * 8;
+        float *o = y + h * 128;
+        for (int l = 0; l < 32; l++) {
+            const int q1 = (a[l] & 15) | ((hb[l] & 3) << 4);
+            const int q2 = (a[l + 32] & 15) | (((hb[l] >> 2) & 3) << 4);
+            const int q3 = (a[l] >> 4) | (((hb[l] >> 4) & 3) << 4);
+            const int q4 = (a[l + 32] >> 4) | (((hb[l] >> 6) & 3) << 4);
+            o[l] = d * s[l / 16] * (q1 - 32);
+            o[l + 32] = d * s[l / 16 + 2] * (q2 - 32);
+            o[l + 64] = d * s[l / 16 + 4] * (q3 - 32);
+            o[l + 96] = d * s[l / 16 + 6] * (q4 - 32);
+        }
+    }
+}
+
 static size_t block_bytes(uint32_t t)
 {
     switch (t) {
     case FORWORD_GGML_Q4_0: return 18;
     case FORWORD_GGML_Q5_0: return 22;
     case FORWORD_GGML_Q8_0: return 34;
+    case FORWORD_GGML_Q4_K: return 144;
+    case FORWORD_GGML_Q6_K: return 210;
     default: return 0;
     }
 }
 
+static size_t block_values(uint32_t t)
+{
+    return t == FORWORD_GGML_Q4_K || t == FORWORD_GGML_Q6_K ? 256 : 32;
+}
+
+static void decode_block(const uint8_t *p, uint32_t type, float *w)
+{
+    if (type == FORWORD_GGML_Q8_0) decode_q8_0(p, w);
+    else if (type == FORWORD_GGML_Q5_0) decode_q5_0(p, w);
+    else if (type == FORWORD_GGML_Q4_K) decode_q4_k(p, w);
+    else if (type == FORWORD_GGML_Q6_K) decode_q6_k(p, w);
+    else decode_q4_0(p, w);
+}
+
 int fwc_dequant(const void *blocks, size_t bytes, uint32_t type, float *out, size_t count)
 {
-    size_t bb = block_bytes(type);
-    if (!blocks || !out || !bb || !bytes || bytes % bb || count % 32 || bytes / bb != count / 32)
+    const size_t bb = block_bytes(type), bv = block_values(type);
+    if (!blocks || !out || !bb || !bytes || bytes % bb || count % bv || bytes / bb != count / bv)
         return -1;
     const uint8_t *p = (const uint8_t *)blocks;
-    for (size_t b = 0; b < bytes / bb; b++, p += bb) {
-        if (type == FORWORD_GGML_Q8_0) decode_q8_0(p, out + 32 * b);
-        else if (type == FORWORD_GGML_Q5_0) decode_q5_0(p, out + 32 * b);
-        else decode_q4_0(p, out + 32 * b);
-    }
+    for (size_t b = 0; b < bytes / bb; b++, p += bb) decode_block(p, type, out + bv * b);
     return 0;
 }
 
-/* dot_quant_block (quant_matvec.c:231-261), with Q4_0 taking the Q5_0 route. */
+/* dot_quant_block (quant_matvec.c:231-261), with Q4_0 taking the Q5_0 route:
+ * decode, then simd_dot_f32 over the block's 32 or 256 values. */
 static float dot_block(const uint8_t *p, uint32_t type, const float *x)
 {
-    float w[32];
+    float w[256];
     if (type == FORWORD_GGML_Q8_0) return dot_q8_0(p, x);
-    if (type == FORWORD_GGML_Q5_0) decode_q5_0(p, w);
-    else decode_q4_0(p, w);
-    return fwc_dot_f32(w, x, 32);
+    decode_block(p, type, w);
+    return fwc_dot_f32(w, x, block_values(type));
 }
 
 /* ── row-parallel driver ─────────────────────────────────────────────────── */
@@ -204,7 +269,7 @@ typedef struct {
     uint32_t type;
     const float *x;
     float *y;
-    size_t in, bpr, bb;
+    size_t in, bpr, bb, bv;
 } qmv_t;
 
 /* quant_matvec row loop (quant_matvec.c:293-309): sequential float sum over blocks. */
@@ -214,7 +279,7 @@ static void qmv_rows(void *c, size_t r0, size_t r1)
     for (size_t r = r0; r < r1; r++) {
         const uint8_t *row = m->w + r * m->bpr * m->bb;
         float sum = 0.0f;
-        for (size_t b = 0; b < m->bpr; b++) sum += dot_block(row + b * m->bb, m->type, m->x + 32 * b);
+        for (size_t b = 0; b < m->bpr; b++) sum += dot_block(row + b * m->bb, m->type, m->x + m->bv * b);
         m->y[r] = sum;
     }
 }
@@ -232,15 +297,16 @@ int fwc_quant_matvec(const void *w, size_t w_size, uint32_t type, const float *x
                      size_t in, size_t out)
 {
     if (!w || !x || !y || !in || !out) return -1;
-    qmv_t m = { (const uint8_t *)w, type, x, y, in, 0, 0 };
+    qmv_t m = { (const uint8_t *)w, type, x, y, in, 0, 0, 0 };
     if (type == FORWORD_GGML_F32) {
         if (out > SIZE_MAX / in / 4 || w_size < out * in * 4) return -1;
         par_rows(f32mv_rows, &m, out);
         return 0;
     }
     m.bb = block_bytes(type);
-    if (!m.bb || in % 32) return -1;
-    m.bpr = in / 32;
+    m.bv = block_values(type);
+    if (!m.bb || in % m.bv) return -1;
+    m.bpr = in / m.bv;
     size_t rb = m.bpr * m.bb;
     if (out > SIZE_MAX / rb || w_size < out * rb) return -1;
     par_rows(qmv_rows, &m, out);
@@ -478,14 +544,14 @@ static int lin(const lin_t *l, const float *x, float *y)
     return fwc_quant_matvec(l->p, l->bytes, l->type, x, y, l->in, l->out);
 }
 
-/* linear_get_row (linear.c:60-151) for F32/Q8_0/Q5_0; Q4_0 by its definition. */
+/* linear_get_row (linear.c:60-151) for F32/Q8_0/Q5_0, Q4_K/Q6_K (linear.c:137-142); Q4_0 by its definition. */
 static int get_row(const lin_t *l, size_t row, float *out)
 {
     if (row >= l->out) return -1;
     if (l->type == FORWORD_GGML_F32) { memcpy(out, l->p + row * l->in * 4, l->in * 4); return 0; }
-    size_t bb = block_bytes(l->type);
-    if (!bb || l->in % 32) return -1;
-    size_t rb = l->in / 32 * bb;
+    const size_t bb = block_bytes(l->type), bv = block_values(l->type);
+    if (!bb || l->in % bv) return -1;
+    const size_t rb = l->in / bv * bb;
     return fwc_dequant(l->p + row * rb, rb, l->type, out, l->in);
 }
 

@@ -78,7 +78,7 @@ def dot(a, b) -> np.float32:
 
 def dequant(blocks: np.ndarray, ggml_type: int) -> np.ndarray:
     blocks = np.ascontiguousarray(blocks, np.uint8)
-    n = blocks.size // fwgpu.BLOCK_BYTES[ggml_type] * 32
+    n = blocks.size // fwgpu.BLOCK_BYTES[ggml_type] * fwgpu.BLOCK_VALUES[ggml_type]
     out = np.empty(n, np.float32)
     if lib().fwc_dequant(blocks.ctypes.data, blocks.size, ggml_type, _f(out), n) != 0:
         raise ValueError("fwc_dequant rejected the input")

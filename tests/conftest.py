@@ -43,5 +43,10 @@ def gold_dequant():
     return load_npz("dequant.npz")
 
 
+@pytest.fixture(scope="session")
+def gold_kquant():
+    return load_npz("kquant.npz")
+
+
 def gold_model(name):
     return load_npz(f"model_{name}.npz")

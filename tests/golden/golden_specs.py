@@ -13,6 +13,7 @@ sys.path.insert(0, os.path.join(ROOT, "forword.c_amd"))
 import fwgpu  # noqa: E402
 
 Q4, Q5, Q8 = fwgpu.GGML_Q4_0, fwgpu.GGML_Q5_0, fwgpu.GGML_Q8_0
+Q4K, Q6K = fwgpu.GGML_Q4_K, fwgpu.GGML_Q6_K
 
 # Model fixtures.  "tiny": dim 288, ffn 768, 6 layers, 6/6 heads, vocab 32000,
 # ctx 256, all Q8_0, theta 1e4, 16-token prompt + 128 greedy tokens.  "gqa":
@@ -133,3 +134,27 @@ def argmax_cases():
     big[[5, 90000, 128255]] = 9.0
     cases.append(big)
     return cases
+
+
+# K-quant fixtures (kquant.npz): super-blocks of random bytes with the fp16 scale
+# fields set from DEQUANT_SCALES (Q4_K: d and dmin; Q6_K: d), decoded by the
+# reference's linear_get_row (linear.c:137-142 -> quant.c:87-188); quant_matvec
+# outputs at these shapes (quant_matvec.c:231-261).
+KQ_TYPES = (Q4K, Q6K)
+KQ_MATVEC_CASES = [(Q4K, 4096, 4096), (Q4K, 4096, 14336), (Q6K, 4096, 4096), (Q6K, 1024, 4096)]
+
+
+def kquant_blocks(t) -> np.ndarray:
+    bb = fwgpu.BLOCK_BYTES[t]
+    rng = np.random.default_rng(200 + t)
+    blocks = []
+    for i, s in enumerate(DEQUANT_SCALES):
+        for k in range(2):
+            b = rng.integers(0, 256, bb).astype(np.uint8)
+            at = 208 if t == Q6K else 0
+            b[at], b[at + 1] = s & 0xFF, s >> 8
+            if t == Q4K:
+                m = DEQUANT_SCALES[(i + 5 + k) % len(DEQUANT_SCALES)]
+                b[2], b[3] = m & 0xFF, m >> 8
+            blocks.append(b)
+    return np.concatenate(blocks)

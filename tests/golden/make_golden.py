@@ -99,6 +99,30 @@ def gen_dequant(tmp, manifest):
     np.savez_compressed(os.path.join(GOLD, "dequant.npz"), **arrays)
 
 
+def gen_kquant(tmp, manifest):
+    arrays = {}
+    for t in gs.KQ_TYPES:
+        blocks = gs.kquant_blocks(t)
+        bp, op = os.path.join(tmp, "b.bin"), os.path.join(tmp, "o.bin")
+        blocks.tofile(bp)
+        n = blocks.size // fwgpu.BLOCK_BYTES[t]
+        run(["getrow", t, 256, n, bp, op])
+        arrays[f"getrow_{t}"] = np.fromfile(op, np.float32)
+        arrays[f"blocks_{t}"] = blocks
+    manifest["kquant"] = {}
+    for (t, rows, cols) in gs.KQ_MATVEC_CASES:
+        w = gs.matvec_weights(t, rows, cols)
+        x = gs.matvec_x(t, rows, cols)
+        wp, xp, yp = (os.path.join(tmp, f) for f in ("w.bin", "x.bin", "y.bin"))
+        w.tofile(wp)
+        x.tofile(xp)
+        run(["qmv", t, cols, rows, wp, xp, yp])
+        key = gs.matvec_key(t, rows, cols)
+        arrays[key] = np.fromfile(yp, np.float32)
+        manifest["kquant"][key] = {"w_sha256": sha(w), "x_sha256": sha(x)}
+    np.savez_compressed(os.path.join(GOLD, "kquant.npz"), **arrays)
+
+
 def gen_ops(tmp, manifest):
     arrays = {}
     p = lambda f: os.path.join(tmp, f)  # noqa: E731
@@ -140,6 +164,16 @@ def gen_ops(tmp, manifest):
 def main():
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "-f", "ref.mk"], check=True)
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "forword.c_amd"), "host"], check=True)
+    only = sys.argv[2] if len(sys.argv) > 2 and sys.argv[1] == "--only" else None
+    if only:                                   # regenerate one fixture file, keep the others
+        with open(os.path.join(GOLD, "manifest.json")) as f:
+            manifest = json.load(f)
+        with tempfile.TemporaryDirectory() as tmp:
+            {"kquant": gen_kquant, "matvec": gen_matvec, "dequant": gen_dequant, "ops": gen_ops}[only](tmp, manifest)
+        with open(os.path.join(GOLD, "manifest.json"), "w") as f:
+            json.dump(manifest, f, indent=1, sort_keys=True)
+        print("fixture", only, "written to", GOLD)
+        return
     manifest = {"generator": "tests/golden/make_golden.py", "reference_build": "oracle/ref.mk",
                 "models": {}, "matvec": {}}
     with tempfile.TemporaryDirectory() as tmp:
@@ -147,6 +181,7 @@ def main():
             gen_model(name, tmp, manifest)
         gen_matvec(tmp, manifest)
         gen_dequant(tmp, manifest)
+        gen_kquant(tmp, manifest)
         gen_ops(tmp, manifest)
     with open(os.path.join(GOLD, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)

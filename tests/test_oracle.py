@@ -147,6 +147,50 @@ def test_dequant_rejects_bad_sizes():
         fw_cpu.dequant(np.zeros(35, np.uint8), Q8)
 
 
+# ── K-quants (Q4_K, Q6_K: 256-value super-blocks) ────────────────────────────────
+
+@pytest.mark.parametrize("t", gs.KQ_TYPES)
+def test_dequant_kquant_matches_reference(t, gold_kquant):
+    blocks = gold_kquant[f"blocks_{t}"]
+    assert np.array_equal(blocks, gs.kquant_blocks(t))
+    assert np.array_equal(bits(fw_cpu.dequant(blocks, t)), bits(gold_kquant[f"getrow_{t}"]))
+
+
+def test_dequant_q4_k_closed_form():
+    """One hand-built Q4_K super-block against quant.c:87-131 written out: d = 2,
+    dmin = 0.5, group j scale j+1 and min 2j (6-bit packing of quant.c:66-85),
+    codes (i + j) % 16."""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(2.0).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    sc, mn = [j + 1 for j in range(8)], [2 * j for j in range(8)]
+    for j in range(4):
+        b[4 + j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        b[8 + j] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        b[12 + j] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    exp = np.zeros(256, np.float32)
+    for j in range(8):
+        for i in range(32):
+            q = (i + j) % 16
+            k = (j // 2) * 32 + i
+            b[16 + k] |= (q << 4) if j & 1 else q
+            exp[32 * j + i] = np.float32(np.float32(2.0 * sc[j]) * np.float32(q)) - np.float32(0.5 * mn[j])
+    assert np.array_equal(bits(fw_cpu.dequant(b, gs.Q4K)), bits(exp))
+
+
+@pytest.mark.parametrize("case", gs.KQ_MATVEC_CASES, ids=lambda c: gs.matvec_key(*c))
+def test_quant_matvec_kquant_matches_reference(case, gold_kquant, manifest):
+    t, rows, cols = case
+    w, x = gs.matvec_weights(t, rows, cols), gs.matvec_x(t, rows, cols)
+    key = gs.matvec_key(t, rows, cols)
+    assert hashlib.sha256(w).hexdigest() == manifest["kquant"][key]["w_sha256"]
+    assert hashlib.sha256(x).hexdigest() == manifest["kquant"][key]["x_sha256"]
+    fw_cpu.set_threads(8)
+    rc, y = fw_cpu.quant_matvec(w, t, x, rows)
+    assert rc == 0
+    assert np.array_equal(bits(y), bits(gold_kquant[key]))
+
+
 # ── quant_matvec ───────────────────────────────────────────────────────────────
 
 @pytest.mark.parametrize("case", gs.MATVEC_CASES, ids=lambda c: gs.matvec_key(*c))
