@@ -194,7 +194,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--config", default="8b", choices=["8b", "lc", "70b", "tiny"])
+    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "tiny"])
     ap.add_argument("--mode", default="full", choices=["full", "decode", "copy"])
     ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -217,6 +217,10 @@ def main():
         sp = fwgpu.spec_8b(n_ctx=max(768, n_ctx))
         workload = ("Llama-3-8B-shape Q4_0 greedy decode at 32K context (Q8_0 embedding/output)" if lc else
                     "Llama-3-8B-shape Q4_0 greedy decode (Q8_0 embedding/output)")
+    elif args.config == "8b-k":
+        sp = fwgpu.spec_8b(n_ctx=max(768, n_ctx), linear_type=fwgpu.GGML_Q4_K, embd_type=fwgpu.GGML_Q4_K,
+                           output_type=fwgpu.GGML_Q6_K)
+        workload = "Llama-3-8B-shape Q4_K greedy decode (Q4_K embedding, Q6_K output)"
     elif args.config == "70b":
         sp = fwgpu.spec_70b(n_ctx=max(384, n_ctx))
         workload = "Llama-3-70B-shape Q4_0 greedy decode (Q8_0 embedding/output)"
@@ -271,7 +275,8 @@ def main():
 
     total_ms, launches = timed_decode(hip, gm, args.steps)
     tok_s = args.steps / (total_ms / 1e3)
-    byte_list = [step_bytes(cfg, p) for p in range(p0, p0 + args.steps)]
+    bb = {"8b-k": dict(linear_bb=18, embd_bb=18, out_bb=26.25)}.get(args.config, {})   # per 32 values
+    byte_list = [step_bytes(cfg, p, **bb) for p in range(p0, p0 + args.steps)]
     avg_bytes = float(np.mean(byte_list))
     log(f"decode: {args.steps} steps at positions {p0}..{p0 + args.steps - 1} in {total_ms:.2f} ms "
         f"-> {tok_s:.1f} tok/s, {avg_bytes * tok_s / 1e9:.0f} GB/s effective")
@@ -337,7 +342,8 @@ def main():
         "config": cfg_out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                     "kernel": f"k_decode (persistent token step, {n_l} steps per launch)",
+                     "kernel": (f"k_decode (persistent token step, {n_l} steps per launch)" if gm_persistent
+                                else f"per-phase step kernels replayed from a hipGraph, {n_l} steps per timing"),
                      "bytes_per_launch": int(launch_bytes), "avg_ms_per_launch": round(launch_ms, 3)},
         "microbench": micro,
         "cpu_baseline": cpu,

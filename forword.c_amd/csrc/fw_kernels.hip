@@ -166,7 +166,36 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
                 if (!ok[k]) continue;
                 const uint8_t *blk = wr[k] + (size_t)sb * SB;
                 float s = 0.f;
-                if constexpr (T == kQ4_K) {
+                if constexpr (T == kQ4_K && PAIR) {                   // dword-aligned super-blocks
+                    const FW_GLOBAL uint32_t *b32 = gptr(reinterpret_cast<const uint32_t *>(blk));
+                    const uint32_t h = b32[0];
+                    const float d = h2f(h), dmin = h2f(h >> 16);
+                    const u32x4 hs = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(b32);   // d|dmin, scales 0..11
+                    const uint32_t sw[3] = { hs.y, hs.z, hs.w };
+                    auto sb8 = [&](uint32_t i) { return (sw[i / 4] >> (8 * (i % 4))) & 0xFFu; };
+                    uint32_t sc, mn;
+                    if (g < 4) { sc = sb8(g) & 63u; mn = sb8(g + 4) & 63u; }
+                    else {
+                        sc = (sb8(g + 4) & 15u) | ((sb8(g - 4) >> 6) << 4);
+                        mn = (sb8(g + 4) >> 4) | ((sb8(g) >> 6) << 4);
+                    }
+                    const float ds = d * (float)sc, dm = dmin * (float)mn;
+                    const FW_GLOBAL uint32_t *q = b32 + 4 + (g / 2) * 8;
+                    uint32_t qw[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i += 4) {
+                        const u32x4 v = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(q + i);
+                        qw[i] = v.x; qw[i + 1] = v.y; qw[i + 2] = v.z; qw[i + 3] = v.w;
+                    }
+                    const uint32_t shift = (g & 1) ? 4u : 0u;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const uint32_t nb = (qw[i] >> shift) & 0x0F0F0F0Fu;
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            s = __builtin_fmaf(ds * (float)((nb >> (8 * e)) & 0xFFu) - dm, xv[4 * i + e], s);
+                    }
+                } else if constexpr (T == kQ4_K) {
                     const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
                     const float dmin = h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
                     uint32_t sc, mn;
@@ -282,6 +311,7 @@ void qmv_plan(QmvArgs &a, int epi)
 
 bool qmv_pair_ok(uint32_t type, uint32_t n_cols, const void *base)
 {
+    if (type == kQ4_K) return ((uintptr_t)base & 3) == 0;          // 144-byte super-blocks stay aligned
     return (type == kQ4_0 || type == kQ5_0 || type == kQ8_0) && n_cols % 64 == 0 && ((uintptr_t)base & 3) == 0;
 }
 
@@ -304,7 +334,7 @@ static hipError_t launch_e(uint32_t type, const QmvArgs &a, hipStream_t s)
     case kQ4_0: return launch_t<kQ4_0, EPI>(a, pair, s);
     case kQ5_0: return launch_t<kQ5_0, EPI>(a, pair, s);
     case kQ8_0: return launch_t<kQ8_0, EPI>(a, pair, s);
-    case kQ4_K: return launch_t<kQ4_K, EPI>(a, false, s);
+    case kQ4_K: return launch_t<kQ4_K, EPI>(a, pair, s);     // pair: dword-aligned super-blocks
     case kQ6_K: return launch_t<kQ6_K, EPI>(a, false, s);
     case kF32: return launch_t<kF32, EPI>(a, false, s);
     default: return hipErrorInvalidValue;
