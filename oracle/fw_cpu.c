@@ -620,3 +620,98 @@ int fwc_generate_greedy(fwc_model_t *m, const uint32_t *prompt, size_t n_prompt,
     }
     return 0;
 }
+
+/* ── sampling (sampler.c:12-101) and the sampled generation loop (main.c:173-217) ── */
+
+static uint64_t xorshift64(uint64_t *s)                       /* sampler.c:8-10 */
+{
+    *s ^= *s << 13;
+    *s ^= *s >> 7;
+    *s ^= *s << 17;
+    return *s;
+}
+
+static const float *g_sort_p;
+/* cmp_prob_desc (sampler.c:40-45) with ties in index order: glibc's qsort is a
+ * stable merge sort for arrays this size, so equal probabilities keep their
+ * index order. */
+static int cmp_desc_stable(const void *a, const void *b)
+{
+    const uint32_t ia = *(const uint32_t *)a, ib = *(const uint32_t *)b;
+    if (g_sort_p[ib] > g_sort_p[ia]) return 1;
+    if (g_sort_p[ib] < g_sort_p[ia]) return -1;
+    return ia < ib ? -1 : ia > ib;
+}
+
+uint32_t fwc_sample(const float *logits, size_t n, const uint32_t *hist, size_t n_hist, float temperature,
+                    float top_p, float penalty, uint64_t *rng)
+{
+    float *p = (float *)malloc(n * sizeof(float));
+    uint32_t *idx = (uint32_t *)malloc(n * sizeof(uint32_t));
+    if (!p || !idx) { free(p); free(idx); return 0; }
+    memcpy(p, logits, n * sizeof(float));
+    if (penalty != 1.0f)                                          /* sampler_rep_penalty, :89-101 */
+        for (size_t i = 0; i < n_hist; i++) {
+            const uint32_t id = hist[i];
+            if (id < n) p[id] = p[id] > 0.0f ? p[id] / penalty : p[id] * penalty;
+        }
+    uint32_t out;
+    if (temperature <= 0.0f) {                                    /* main.c:184-185 */
+        out = fwc_argmax(p, n);
+    } else {                                                      /* sampler_top_p, :47-87 */
+        if (temperature != 1.0f) {
+            const float inv = 1.0f / temperature;
+            for (size_t i = 0; i < n; i++) p[i] *= inv;
+        }
+        float mx = p[0];                                          /* sampler_softmax, :18-26 */
+        for (size_t i = 1; i < n; i++) if (p[i] > mx) mx = p[i];
+        float sum = 0.0f;
+        for (size_t i = 0; i < n; i++) { p[i] = expf(p[i] - mx); sum += p[i]; }
+        const float inv = 1.0f / sum;
+        for (size_t i = 0; i < n; i++) p[i] *= inv;
+        for (size_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
+        g_sort_p = p;
+        qsort(idx, n, sizeof(uint32_t), cmp_desc_stable);
+        float cum = 0.0f;
+        size_t nucleus = 0;
+        for (size_t i = 0; i < n; i++) {
+            cum += p[idx[i]];
+            nucleus = i + 1;
+            if (cum >= top_p) break;
+        }
+        float norm = 0.0f;
+        for (size_t i = 0; i < nucleus; i++) norm += p[idx[i]];
+        const float r = (float)(xorshift64(rng) >> 11) / (float)(UINT64_MAX >> 11) * norm;
+        out = idx[nucleus - 1];
+        cum = 0.0f;
+        for (size_t i = 0; i < nucleus; i++) {
+            cum += p[idx[i]];
+            if (r <= cum) { out = idx[i]; break; }
+        }
+    }
+    free(p);
+    free(idx);
+    return out;
+}
+
+int fwc_generate_sampled(fwc_model_t *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen, float temperature,
+                         float top_p, float penalty, uint64_t seed, uint32_t *out_ids)
+{
+    if (!m || !prompt || !n_prompt || !out_ids) return -1;
+    uint64_t rng = seed ? seed : 12345;                           /* main.c:98-99 */
+    uint32_t *hist = (uint32_t *)malloc((n_prompt + n_gen) * sizeof(uint32_t));
+    if (!hist) return -1;
+    memcpy(hist, prompt, n_prompt * sizeof(uint32_t));
+    size_t n_hist = n_prompt;
+    float *lg = NULL;
+    for (size_t i = 0; i < n_prompt; i++)
+        if (!(lg = fwc_forward(m, prompt[i], i))) { free(hist); return -1; }
+    for (size_t g = 0; g < n_gen; g++) {
+        const uint32_t t = fwc_sample(lg, m->c.n_vocab, hist, n_hist, temperature, top_p, penalty, &rng);
+        out_ids[g] = t;
+        hist[n_hist++] = t;
+        if (g + 1 < n_gen && !(lg = fwc_forward(m, t, n_prompt + g))) { free(hist); return -1; }
+    }
+    free(hist);
+    return 0;
+}

@@ -70,6 +70,13 @@ float   *fwc_kv_v(fwc_model_t *m, size_t layer, size_t pos);
 /* prefill + greedy (rep-pen 1.0, no EOS): out_ids[n_gen] */
 int      fwc_generate_greedy(fwc_model_t *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                              uint32_t *out_ids);
+/* one sampling decision (sampler.c:12-101, main.c:176-188): repetition penalty over
+ * hist, then argmax (temperature <= 0) or top-p with the xorshift64 state *rng */
+uint32_t fwc_sample(const float *logits, size_t n, const uint32_t *hist, size_t n_hist, float temperature,
+                    float top_p, float penalty, uint64_t *rng);
+/* prefill + sampled generation (main.c:145-217 without EOS/stop strings), seed 0 -> 12345 */
+int      fwc_generate_sampled(fwc_model_t *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                              float temperature, float top_p, float penalty, uint64_t seed, uint32_t *out_ids);
 
 #ifdef __cplusplus
 }

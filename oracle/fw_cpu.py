@@ -47,6 +47,10 @@ def lib():
         s(L, "fwc_kv_k", fp, [vp, sz, sz])
         s(L, "fwc_kv_v", fp, [vp, sz, sz])
         s(L, "fwc_generate_greedy", C.c_int, [vp, u32p, sz, sz, u32p])
+        s(L, "fwc_sample", C.c_uint32, [fp, sz, u32p, sz, C.c_float, C.c_float, C.c_float,
+                                        C.POINTER(C.c_uint64)])
+        s(L, "fwc_generate_sampled", C.c_int, [vp, u32p, sz, sz, C.c_float, C.c_float, C.c_float, C.c_uint64,
+                                               u32p])
         _lib = L
     return _lib
 
@@ -180,6 +184,15 @@ class OracleModel:
             raise ValueError("fwc_generate_greedy failed")
         return out
 
+    def generate_sampled(self, prompt, n_gen: int, temperature: float, top_p: float, penalty: float,
+                         seed: int) -> np.ndarray:
+        pr = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_gen, np.uint32)
+        if lib().fwc_generate_sampled(self.m, pr.ctypes.data_as(u32p), pr.size, n_gen, temperature, top_p,
+                                      penalty, seed, out.ctypes.data_as(u32p)) != 0:
+            raise ValueError("fwc_generate_sampled failed")
+        return out
+
     def close(self):
         if getattr(self, "m", None):
             lib().fwc_model_free(self.m)
@@ -190,3 +203,13 @@ class OracleModel:
 
     def __exit__(self, *a):
         self.close()
+
+
+def sample(logits, hist, temperature, top_p, penalty, rng_state: int):
+    """One sampling decision; returns (token, new xorshift64 state)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    h = np.ascontiguousarray(hist, np.uint32)
+    st = C.c_uint64(rng_state)
+    t = lib().fwc_sample(_f(lg), lg.size, h.ctypes.data_as(u32p), h.size, temperature, top_p, penalty,
+                         C.byref(st))
+    return int(t), int(st.value)

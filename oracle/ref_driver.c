@@ -21,6 +21,11 @@
  *   dot N A B OUT                   simd_dot_f32 (simd.h:27-155)
  *   argmax N X OUT                  sampler_argmax (sampler.c:28-32)
  *   q8dec NBYTES IN OUT             q8_0_decode (quant.c:232-263)
+ *   sample N TEMP TOPP PEN SEED NHIST LOGITS HIST OUT
+ *                                   one decision as main.c:176-188: sampler_rep_penalty
+ *                                   over HIST, then sampler_argmax (TEMP <= 0) or
+ *                                   sampler_top_p (sampler.c:47-101); OUT = token (u32)
+ *                                   and the xorshift64 state after it (u64)
  */
 #define _POSIX_C_SOURCE 200809L
 #include <math.h>
@@ -250,6 +255,20 @@ int main(int argc, char **argv)
         float *o = (float *)calloc(n / 34 * 32, 4);
         if (q8_0_decode(in, n, o, n / 34 * 32)) return 6;
         spit(argv[4], o, n / 34 * 32 * 4);
+        return 0;
+    }
+    if (!strcmp(m, "sample") && argc == 11) {
+        size_t n = strtoul(argv[2], NULL, 10), nh = strtoul(argv[7], NULL, 10);
+        float temp = strtof(argv[3], NULL), top_p = strtof(argv[4], NULL), pen = strtof(argv[5], NULL);
+        uint64_t rng = strtoull(argv[6], NULL, 10);
+        float *lg = (float *)slurp(argv[8], NULL);
+        uint32_t *hist = nh ? (uint32_t *)slurp(argv[9], NULL) : NULL;
+        sampler_rep_penalty(lg, n, hist, nh, pen);
+        uint32_t tok = temp <= 0.0f ? sampler_argmax(lg, n) : sampler_top_p(lg, n, temp, top_p, &rng);
+        unsigned char out[12];
+        memcpy(out, &tok, 4);
+        memcpy(out + 4, &rng, 8);
+        spit(argv[10], out, 12);
         return 0;
     }
     fprintf(stderr, "ref_driver: bad mode/arguments\n");

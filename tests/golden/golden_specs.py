@@ -158,3 +158,22 @@ def kquant_blocks(t) -> np.ndarray:
                 b[2], b[3] = m & 0xFF, m >> 8
             blocks.append(b)
     return np.concatenate(blocks)
+
+
+# sampler fixtures (sampler.npz): logits vectors x settings, one reference decision each
+SAMPLE_SETTINGS = [(0.0, 0.9, 1.0), (0.0, 0.9, 1.3), (0.8, 0.9, 1.0), (0.8, 0.9, 1.1), (1.0, 1.0, 1.0),
+                   (0.5, 0.5, 1.2), (1.5, 0.95, 1.05), (0.7, 0.2, 1.0)]
+SAMPLE_SEEDS = [12345, 987654321, 2 ** 63 + 77]
+
+
+def sample_cases():
+    """(name, logits, hist) triples: spread-out, peaked, tied and large-vocabulary logits."""
+    rng = np.random.default_rng(31)
+    ties = rng.standard_normal(500).astype(np.float32)
+    ties[100:140] = ties[3]                                       # equal probabilities
+    peaked = (rng.standard_normal(4000) * 4.0).astype(np.float32)
+    return [("n1000", rng.standard_normal(1000).astype(np.float32), rng.integers(0, 1000, 40).astype(np.uint32)),
+            ("ties", ties, np.array([3, 3, 3, 7, 120, 499], np.uint32)),
+            ("peaked", peaked, rng.integers(0, 4000, 200).astype(np.uint32)),
+            ("v32000", rng.standard_normal(32000).astype(np.float32) * 2.0,
+             rng.integers(0, 32000, 64).astype(np.uint32))]

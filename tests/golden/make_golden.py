@@ -123,6 +123,25 @@ def gen_kquant(tmp, manifest):
     np.savez_compressed(os.path.join(GOLD, "kquant.npz"), **arrays)
 
 
+def gen_sampler(tmp, manifest):
+    arrays = {}
+    for name, lg, hist in gs.sample_cases():
+        arrays[f"logits_{name}"] = lg
+        arrays[f"hist_{name}"] = hist
+        res = []
+        for (temp, top_p, pen) in gs.SAMPLE_SETTINGS:
+            for seed in gs.SAMPLE_SEEDS:
+                lp, hp, op = (os.path.join(tmp, f) for f in ("l.bin", "h.bin", "o.bin"))
+                lg.tofile(lp)
+                hist.tofile(hp)
+                run(["sample", lg.size, repr(temp), repr(top_p), repr(pen), seed, hist.size, lp, hp, op])
+                raw = np.fromfile(op, np.uint8)
+                res.append((int(raw[:4].view(np.uint32)[0]), int(raw[4:12].view(np.uint64)[0])))
+        arrays[f"tok_{name}"] = np.array([r[0] for r in res], np.uint32)
+        arrays[f"rng_{name}"] = np.array([r[1] for r in res], np.uint64)
+    np.savez_compressed(os.path.join(GOLD, "sampler.npz"), **arrays)
+
+
 def gen_ops(tmp, manifest):
     arrays = {}
     p = lambda f: os.path.join(tmp, f)  # noqa: E731
@@ -169,7 +188,8 @@ def main():
         with open(os.path.join(GOLD, "manifest.json")) as f:
             manifest = json.load(f)
         with tempfile.TemporaryDirectory() as tmp:
-            {"kquant": gen_kquant, "matvec": gen_matvec, "dequant": gen_dequant, "ops": gen_ops}[only](tmp, manifest)
+            {"kquant": gen_kquant, "sampler": gen_sampler, "matvec": gen_matvec, "dequant": gen_dequant,
+             "ops": gen_ops}[only](tmp, manifest)
         with open(os.path.join(GOLD, "manifest.json"), "w") as f:
             json.dump(manifest, f, indent=1, sort_keys=True)
         print("fixture", only, "written to", GOLD)
@@ -182,6 +202,7 @@ def main():
         gen_matvec(tmp, manifest)
         gen_dequant(tmp, manifest)
         gen_kquant(tmp, manifest)
+        gen_sampler(tmp, manifest)
         gen_ops(tmp, manifest)
     with open(os.path.join(GOLD, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)

@@ -10,7 +10,7 @@ import pytest
 import fw_cpu
 import fwgpu
 import golden_specs as gs
-from conftest import gold_model
+from conftest import gold_model, load_npz
 
 Q4, Q5, Q8 = fwgpu.GGML_Q4_0, fwgpu.GGML_Q5_0, fwgpu.GGML_Q8_0
 
@@ -338,3 +338,18 @@ def test_forward_rejects_out_of_range():                       # transformer.c:1
         assert not om.forward_raw(0, host.n_ctx)
         assert not om.forward_raw(host.cfg.n_vocab, 0)
         assert om.forward_raw(host.cfg.n_vocab - 1, host.n_ctx - 1)
+
+
+# ── sampler (sampler.c:12-101 as main.c:176-188 calls it) ─────────────────────────
+
+def test_sampler_matches_reference():
+    gold = load_npz("sampler.npz")
+    for name, lg, hist in gs.sample_cases():
+        assert np.array_equal(gold[f"logits_{name}"], lg) and np.array_equal(gold[f"hist_{name}"], hist)
+        k = 0
+        for (temp, top_p, pen) in gs.SAMPLE_SETTINGS:
+            for seed in gs.SAMPLE_SEEDS:
+                tok, st = fw_cpu.sample(lg, hist, temp, top_p, pen, seed)
+                assert tok == int(gold[f"tok_{name}"][k]), (name, temp, top_p, pen, seed)
+                assert st == int(gold[f"rng_{name}"][k]), (name, temp, top_p, pen, seed)
+                k += 1
