@@ -123,6 +123,11 @@ struct forword_gpu {
     MkLayer *d_layers = nullptr;
     uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
     uint32_t prof_steps = 0;
+    // sampled generation (allocated on first use): probabilities, reductions, buckets,
+    // history counts, PRNG state, sampled ids
+    float *d_sbuf = nullptr, *d_spart = nullptr, *d_bsum = nullptr;
+    uint32_t *d_bcnt = nullptr, *d_counts = nullptr, *d_sids = nullptr;
+    SampleState *d_ss = nullptr;
     // batched prefill: activations of up to kPrefillChunk tokens (allocated on first use)
     float *d_pf = nullptr;
     uint32_t *d_pf_tok = nullptr;
@@ -795,6 +800,70 @@ extern "C" int forword_gpu_prefill_argmax(forword_gpu_t *h, const uint32_t *toke
     HIPCHK(hipMemcpyAsync(h->h_u32, h->d_argmax, 4, hipMemcpyDeviceToHost, h->stream), "argmax download");
     HIPCHK(hipStreamSynchronize(h->stream), "prefill_argmax");
     *next = h->h_u32[0];
+    return 0;
+}
+
+// ── sampled generation ───────────────────────────────────────────────────────
+
+// Candidates the top-p sort holds (LDS of one workgroup).
+static constexpr uint32_t kSampleCap = 16384;
+
+extern "C" int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                                    float temperature, float top_p, float repetition_penalty, uint64_t seed,
+                                    uint32_t *out_ids)
+{
+    if (!h || !prompt || !n_prompt || !n_gen || !out_ids) { set_err("generate: invalid arguments"); return -1; }
+    const uint32_t nv = h->cfg.n_vocab;
+    const size_t n_fwd = n_prompt + n_gen - 1;
+    if (n_fwd > h->n_ctx) { set_err("generate: %zu forwards exceed the KV cache (%zu)", n_fwd, h->n_ctx); return -1; }
+    for (size_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= nv) { set_err("generate: prompt token %u out of range", prompt[i]); return -1; }
+    if (!h->d_sbuf) {
+        if (dalloc(h, (void **)&h->d_sbuf, (size_t)nv * 4, "sampler probabilities") ||
+            dalloc(h, (void **)&h->d_spart, 512 * 4, "sampler partials") ||
+            dalloc(h, (void **)&h->d_bsum, 1024 * 4, "sampler buckets") ||
+            dalloc(h, (void **)&h->d_bcnt, 1024 * 4, "sampler buckets") ||
+            dalloc(h, (void **)&h->d_counts, (size_t)nv * 4, "history counts") ||
+            dalloc(h, (void **)&h->d_sids, (h->n_ctx + 1) * 4, "sampled ids") ||
+            dalloc(h, (void **)&h->d_ss, sizeof(SampleState), "sampler state"))
+            return -1;
+        HIPCHK(hipMemset(h->d_bsum, 0, 1024 * 4), "sampler buckets");
+        HIPCHK(hipMemset(h->d_bcnt, 0, 1024 * 4), "sampler buckets");
+    }
+    // history counts of the prompt (main.c:157-161) and the PRNG seed (main.c:98-99)
+    std::vector<uint32_t> counts(nv, 0u);
+    for (size_t i = 0; i < n_prompt; i++) counts[prompt[i]]++;
+    SampleState ss{};
+    ss.rng = seed ? seed : 12345u;
+    HIPCHK(hipMemcpyAsync(h->d_counts, counts.data(), (size_t)nv * 4, hipMemcpyHostToDevice, h->stream), "counts upload");
+    HIPCHK(hipMemcpyAsync(h->d_ss, &ss, sizeof ss, hipMemcpyHostToDevice, h->stream), "sampler state upload");
+    // the prompt as generate_greedy feeds it (main.c:145-151); the last step leaves its logits
+    HIPCHK(hipMemcpyAsync(h->d_prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice, h->stream), "prompt upload");
+    h->h_state->token = prompt[0];
+    h->h_state->pos = 0;
+    h->h_state->n_prompt = (uint32_t)n_prompt;
+    h->h_state->next = 0;
+    h->h_state->greedy = 1;
+    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    if (run_steps(h, n_prompt)) return -1;
+    // main.c:173-217: sample from the logits on the device, forward the sample
+    for (size_t g = 0; g < n_gen; g++) {
+        HIPCHK(launch_sample(h->d_logits, nv, h->d_counts, temperature, top_p, repetition_penalty, h->d_sbuf,
+                             h->d_spart, h->d_bcnt, h->d_bsum, kSampleCap, h->d_ss, h->d_state, h->d_sids,
+                             (uint32_t)g, h->d_counts, h->stream),
+               "sampler launch");
+        if (g + 1 < n_gen && run_steps(h, 1)) return -1;
+    }
+    HIPCHK(hipMemcpyAsync(out_ids, h->d_sids, n_gen * 4, hipMemcpyDeviceToHost, h->stream), "ids download");
+    HIPCHK(hipMemcpyAsync(&ss, h->d_ss, sizeof ss, hipMemcpyDeviceToHost, h->stream), "sampler state download");
+    HIPCHK(hipStreamSynchronize(h->stream), "generate");
+    if (mk_check(h)) return -1;
+    h->h_state->pos = (uint32_t)n_fwd;
+    h->traced = true;
+    if (ss.err) {
+        set_err("generate: a top-p nucleus did not fit the %u-candidate sort (lower top_p or temperature)", kSampleCap);
+        return -1;
+    }
     return 0;
 }
 

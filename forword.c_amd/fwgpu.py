@@ -157,6 +157,7 @@ def gpu_lib():
         _sig(L, "forword_gpu_decode", C.c_int, [vp, sz, u32p])
         _sig(L, "forword_gpu_decode_from", C.c_int, [vp, u32, sz, sz, u32p])
         _sig(L, "forword_gpu_prefill", fp, [vp, u32p, sz, sz])
+        _sig(L, "forword_gpu_generate", C.c_int, [vp, u32p, sz, sz, f32, f32, f32, u64, u32p])
         _sig(L, "forword_gpu_prefill_argmax", C.c_int, [vp, u32p, sz, sz, u32p])
         _sig(L, "forword_gpu_ffn_swiglu", C.c_int, [vp, vp, sz, u32, vp, vp, sz, sz, vp])
         _sig(L, "forword_gpu_kv_write", C.c_int, [vp, sz, sz, sz, fp, fp])
@@ -367,6 +368,15 @@ class GpuModel:
         _check(gpu_lib().forword_gpu_prefill_argmax(self.h, tk.ctypes.data_as(u32p), tk.size, pos0, C.byref(nxt)),
                "prefill_argmax")
         return nxt.value
+
+    def generate(self, prompt, n_gen: int, temperature: float = 0.8, top_p: float = 0.9,
+                 repetition_penalty: float = 1.1, seed: int = 12345) -> np.ndarray:
+        """The CLI's sampled generation loop (main.c:145-217, sampler.c) on the device."""
+        pr = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_gen, np.uint32)
+        _check(gpu_lib().forword_gpu_generate(self.h, pr.ctypes.data_as(u32p), pr.size, n_gen, temperature, top_p,
+                                              repetition_penalty, seed, out.ctypes.data_as(u32p)), "generate")
+        return out
 
     def generate_greedy_batched(self, prompt, n_gen: int) -> np.ndarray:
         """Greedy generation with the batched prefill: the prompt in one pass, then

@@ -122,6 +122,23 @@ int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *prompt, size_t
                                 size_t n_gen, uint32_t *out_ids);
 
 /*
+ * The CLI's generation loop with its sampler, device-resident (main.c:145-217
+ * with sampler.c:12-101): prompt[0..n_prompt) token by token, then n_gen
+ * tokens, each drawn from the current logits after the repetition penalty over
+ * the prompt and the tokens drawn so far (sampler_rep_penalty, once per
+ * occurrence), greedily when temperature <= 0 (sampler_argmax) or by top-p with
+ * the xorshift64 stream seeded by `seed` (0 -> 12345 as main.c:98-99).  No EOS or
+ * stop-string check (main.c:190-208 is the caller's): out_ids[0..n_gen) are the
+ * drawn tokens.  Draws equal the reference's except where the random number
+ * falls within float rounding of a cumulative-probability boundary (the softmax
+ * normaliser is a parallel sum).  -1 when a top-p nucleus holds more than 16384
+ * tokens.  Costs n_prompt + n_gen - 1 forwards.
+ */
+int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                         float temperature, float top_p, float repetition_penalty, uint64_t seed,
+                         uint32_t *out_ids);
+
+/*
  * Continue the greedy loop of the last forword_gpu_generate_greedy for n_steps
  * more forwards, each fed the previous argmax (main.c:173-217, decode part).
  * With out_ids != NULL the n_steps new tokens are copied out and the call
