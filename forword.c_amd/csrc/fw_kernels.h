@@ -39,6 +39,7 @@ struct QmvArgs {
                                // RESID: residual stream x (updated in place); SWIGLU: h
     float *trace;              // RESID: copy of the updated residual (may be null)
     const float *cos_tab, *sin_tab;
+    const float *bias[3];      // QKV: F32 bias by role (attn_{q,k,v}.bias) added before RoPE, or null
     const StepState *state;
     uint32_t head_dim;
     uint32_t kv_dim;           // n_head_kv * head_dim (K/V cache row length)
@@ -134,7 +135,8 @@ hipError_t launch_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols, c
                              uint32_t n_tok, float embd_scale, float *x, hipStream_t s);
 // Rows [q | k | v] ld floats apart at positions pos0..: RoPE on q in place, K
 // (rotated) and V appended to the layer's cache rows.
-hipError_t launch_rope_append(float *qkv, uint32_t ld, uint32_t n_tok, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+hipError_t launch_rope_append(float *qkv, const float *bias, uint32_t ld, uint32_t n_tok, uint32_t n_head,
+                              uint32_t n_kv, uint32_t hd,
                               uint32_t pos0, const float *cos_tab, const float *sin_tab, float *kc_layer,
                               float *vc_layer, hipStream_t s);
 // Causal attention of the n_tok rows' queries over cache rows 0..pos0+t.

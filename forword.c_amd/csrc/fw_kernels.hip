@@ -266,13 +266,14 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
 #pragma unroll
             for (int k = 0; k < R / 2; k++)
                 if (ok[k]) a.out[0][row[k]] = silu_ref(acc[k]) * acc[k + R / 2];   // ffn.c:88-104
-    } else {   // EPI_QKV: RoPE on q and k rows (rope.c:37-43), then q out / KV append at pos
+    } else {   // EPI_QKV: bias (linear.c:214-221), RoPE on q and k rows (rope.c:37-43), q out / KV append at pos
         if (lane == 0 && active) {
             const uint32_t pos = a.state->pos, half = a.head_dim / 2;
             const uint32_t role = seg + a.role_base;
+            const float *bias = a.bias[role];
             float v[R];
 #pragma unroll
-            for (int k = 0; k < R; k++) v[k] = acc[k];
+            for (int k = 0; k < R; k++) v[k] = bias && ok[k] ? acc[k] + bias[row[k]] : acc[k];
             if (role < 2) {
 #pragma unroll
                 for (int k = 0; k < R; k += 2) {

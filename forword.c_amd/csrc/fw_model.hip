@@ -61,6 +61,7 @@ struct Lin {
 
 struct Layer {
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    const float *bqkv = nullptr;   // attn_q|k|v.bias concatenated [n_embd + 2 kv_dim] (qwen2), or null
     Lin q, k, v, o, gate, up, down;
 };
 
@@ -104,6 +105,7 @@ struct forword_gpu {
     float *d_logits = nullptr, *d_part = nullptr, *d_trace = nullptr, *d_pv = nullptr;
     uint32_t *d_pi = nullptr, *d_counter = nullptr, *d_argmax = nullptr, *d_prompt = nullptr, *d_ids = nullptr;
     float *d_pss = nullptr, *d_scale = nullptr;      // RMSNorm scale published by the residual kernels
+    float *d_bias = nullptr;                         // per-layer q|k|v biases (qwen2)
     uint32_t *d_ticket = nullptr;
     StepState *d_state = nullptr, *h_state = nullptr;
     float *h_logits = nullptr;
@@ -233,6 +235,7 @@ static hipError_t enqueue_step(forword_gpu_t *h)
             a.norm_w = Ly.attn_norm; a.norm_scale = h->d_scale;
             a.out[0] = h->d_q; a.out[1] = kc; a.out[2] = vc;
             a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
+            if (Ly.bqkv) { a.bias[0] = Ly.bqkv; a.bias[1] = Ly.bqkv + n; a.bias[2] = Ly.bqkv + n + kvd; }
             a.state = h->d_state;
             a.head_dim = hd;
             a.kv_dim = kvd;
@@ -357,6 +360,7 @@ static int setup_mk(forword_gpu_t *h)
     a.n_embd = n; a.n_ff = c.n_ff; a.n_head = c.n_head; a.n_kv = c.n_head_kv; a.head_dim = hd;
     a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
     a.kc = h->d_k; a.vc = h->d_v; a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
+    a.bqkv = h->d_bias;
     a.q = h->d_q; a.logits = h->d_logits; a.trace = h->d_trace;
     a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
     // (KV head, split) attention items: about one per workgroup, >= 8 positions per split
@@ -476,8 +480,8 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         return -1;
     }
     if (c.norm_type != FORWORD_NORM_RMS || c.act_type != FORWORD_ACT_SILU || !c.use_ffn_gate ||
-        c.use_qkv_bias || c.parallel_res || c.rope_type != FORWORD_ROPE_NORMAL) {
-        set_err("forword_gpu_init: only the llama block (RMSNorm, SwiGLU, RoPE pairs (2i,2i+1), no biases, "
+        c.parallel_res || c.rope_type != FORWORD_ROPE_NORMAL) {
+        set_err("forword_gpu_init: only the llama/qwen2 block (RMSNorm, SwiGLU, RoPE pairs (2i,2i+1), "
                 "sequential residual) is implemented");
         return -1;
     }
@@ -536,6 +540,33 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         if (bind_vec(h, &Ly.attn_norm, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);
         if (bind_vec(h, &Ly.ffn_norm, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
+        snprintf(nm, sizeof nm, "blk.%u.attn_output.bias", l);                        // attention.c:106-107
+        if (find_t(tensors, n_tensors, nm)) { set_err("tensor %s: output-projection bias not implemented", nm); FAIL(); }
+    }
+    if (c.use_qkv_bias) {
+        // attention.c:114-122: the q/k/v biases of each layer, gathered into one
+        // [n_embd | kv_dim | kv_dim] vector in the order the fused QKV rows use;
+        // a missing one adds nothing (zeros).  linear.c:214-221 adds F32 biases only.
+        const size_t per = (size_t)n + 2 * kvd;
+        if (dalloc(h, (void **)&h->d_bias, c.n_layer * per * 4, "qkv bias") ||
+            hipMemset(h->d_bias, 0, c.n_layer * per * 4) != hipSuccess)
+            FAIL();
+        static const char *const sfx[3] = { "attn_q.bias", "attn_k.bias", "attn_v.bias" };
+        for (uint32_t l = 0; l < c.n_layer; l++) {
+            float *dst = h->d_bias + l * per;
+            const size_t off[3] = { 0, n, (size_t)n + kvd }, len[3] = { n, kvd, kvd };
+            for (int r = 0; r < 3; r++) {
+                char nm[96];
+                snprintf(nm, sizeof nm, "blk.%u.%s", l, sfx[r]);
+                const float *b = nullptr;
+                if (bind_vec(h, &b, find_t(tensors, n_tensors, nm), nm, len[r], false)) FAIL();
+                if (b && hipMemcpy(dst + off[r], b, len[r] * 4, hipMemcpyDeviceToDevice) != hipSuccess) {
+                    set_err("qkv bias copy failed");
+                    FAIL();
+                }
+            }
+            h->L[l].bqkv = dst;
+        }
     }
 
     const size_t kv_elems = (size_t)c.n_layer * max_ctx * kvd, half = hd / 2;
@@ -752,7 +783,7 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
                 TRY(launch_gemm_q(Ly.v.type, Xn, n, Ly.v.w, Ly.v.row_bytes, QKV + nq + kvd, ldqkv, rows, kvd, n, false,
                                   s));
             }
-            TRY(launch_rope_append(QKV, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
+            TRY(launch_rope_append(QKV, Ly.bqkv, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
             TRY(launch_attn_prefill(QKV, ldqkv, rows, kc, vc, Att, c.n_head, c.n_head_kv, hd, p0, s));
             TRY(launch_gemm_q(Ly.o.type, Att, nq, Ly.o.w, Ly.o.row_bytes, X, n, rows, n, nq, true, s));   // :271-272
             TRY(launch_rmsnorm_rows(X, Ly.ffn_norm, Xn, n, rows, c.norm_eps, s));             // :275

@@ -318,11 +318,12 @@ hipError_t launch_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols, c
 // ── RoPE on q and k, K/V append ─────────────────────────────────────────────
 
 // QKV[t] = [q (n_head·hd) | k (kvd) | v (kvd)] of token t at position pos0 + t:
-// rotate q in place and k (rope.c:37-43, interleaved pairs), append k and v to
-// the cache rows (attention.c:129-140).
-__global__ __launch_bounds__(256) void k_rope_append(float *qkv, uint32_t ld, uint32_t n_head, uint32_t n_kv,
-                                                     uint32_t hd, uint32_t pos0, const float *cos_tab,
-                                                     const float *sin_tab, float *kc, float *vc)
+// add the bias of the same layout when there is one (linear.c:214-221), rotate
+// q in place and k (rope.c:37-43, interleaved pairs), append k and v to the
+// cache rows (attention.c:129-140).
+__global__ __launch_bounds__(256) void k_rope_append(float *qkv, const float *bias, uint32_t ld, uint32_t n_head,
+                                                     uint32_t n_kv, uint32_t hd, uint32_t pos0,
+                                                     const float *cos_tab, const float *sin_tab, float *kc, float *vc)
 {
     const uint32_t t = blockIdx.y, half = hd / 2, pos = pos0 + t, kvd = n_kv * hd;
     float *row = qkv + (size_t)t * ld;
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(256) void k_rope_append(float *qkv, uint32_t ld, ui
         const uint32_t p = i % half;
         float *v = row + 2 * (size_t)i;          // pairs of q, then of k (contiguous)
         const float c = cos_tab[(size_t)pos * half + p], s = sin_tab[(size_t)pos * half + p];
-        const float v0 = v[0], v1 = v[1];
+        const float v0 = bias ? v[0] + bias[2 * i] : v[0], v1 = bias ? v[1] + bias[2 * i + 1] : v[1];
         const float w0 = v0 * c - v1 * s, w1 = v0 * s + v1 * c;
         if (i < n_head * half) {
             v[0] = w0;
@@ -344,18 +345,19 @@ __global__ __launch_bounds__(256) void k_rope_append(float *qkv, uint32_t ld, ui
         }
     } else if (i < n_pairs + kvd / 2) {
         const uint32_t e = 2 * (i - n_pairs);
-        const float *vv = row + (size_t)n_head * hd + kvd + e;
-        vc[(size_t)pos * kvd + e] = vv[0];
-        vc[(size_t)pos * kvd + e + 1] = vv[1];
+        const size_t o = (size_t)n_head * hd + kvd + e;
+        vc[(size_t)pos * kvd + e] = bias ? row[o] + bias[o] : row[o];
+        vc[(size_t)pos * kvd + e + 1] = bias ? row[o + 1] + bias[o + 1] : row[o + 1];
     }
 }
 
-hipError_t launch_rope_append(float *qkv, uint32_t ld, uint32_t n_tok, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+hipError_t launch_rope_append(float *qkv, const float *bias, uint32_t ld, uint32_t n_tok, uint32_t n_head,
+                              uint32_t n_kv, uint32_t hd,
                               uint32_t pos0, const float *cos_tab, const float *sin_tab, float *kc_layer,
                               float *vc_layer, hipStream_t s)
 {
     const uint32_t n = (n_head + n_kv) * (hd / 2) + n_kv * hd / 2;
-    hipLaunchKernelGGL(k_rope_append, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, ld, n_head, n_kv, hd, pos0,
+    hipLaunchKernelGGL(k_rope_append, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, bias, ld, n_head, n_kv, hd, pos0,
                        cos_tab, sin_tab, kc_layer, vc_layer);
     return hipGetLastError();
 }

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ bu
 {
     extern __shared__ uint64_t keys[];
     __shared__ float s_v[16];
-    __shared__ uint32_t s_i[16], s_sel, s_cnt, s_n, s_tok;
+    __shared__ uint32_t s_i[16], s_sel, s_n, s_tok;
     const uint32_t t = threadIdx.x, lane = t & 63, w = t >> 6;
     if (temperature <= 0.0f) {
         float bv = -INFINITY;
@@ -141,10 +141,8 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ bu
             uint32_t b = kSampBuckets, cnt = 0;
             while (b > 0 && acc < top_p) { b--; acc += bsum[b]; cnt += bcnt[b]; }
             uint32_t sel = b > 0 ? b - 1 : 0;                        // one bucket of margin
-            uint32_t c2 = cnt + (b > 0 ? bcnt[b - 1] : 0);
-            if (c2 > cap) { sel = b; c2 = cnt; }
+            if (cnt + (b > 0 ? bcnt[b - 1] : 0) > cap) sel = b;          // no room for the margin
             s_sel = sel;
-            s_cnt = c2;
             s_n = 0;
         }
         __syncthreads();

@@ -46,6 +46,7 @@ struct MkArgs {
     float eps;
     float *kc, *vc;
     const float *cos_tab, *sin_tab;
+    const float *bqkv;       // [n_layer][n_embd + 2 kv_dim] attn_q|k|v.bias per layer, or null
     float *q, *logits;
     // Activations passed between phases without a grid barrier, as {value,
     // epoch} words (see tagged()): residual stream x, attention output, ffn h.

@@ -637,10 +637,11 @@ __device__ __forceinline__ void wg_rows(uint32_t n_rows, uint32_t &lo, uint32_t 
 
 // ── epilogues ────────────────────────────────────────────────────────────────
 
-// RoPE on q/k rows (rope.c:37-43) with this position's cos/sin (rope[0..hd/2)
-// and rope[hd/2..hd) in LDS), q store, K/V append at pos (attention.c:129-140).
+// Bias (linear.c:214-221; bias null when the model has none), RoPE on q/k rows
+// (rope.c:37-43) with this position's cos/sin (rope[0..hd/2) and rope[hd/2..hd)
+// in LDS), q store, K/V append at pos (attention.c:129-140).
 __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const float *part, const float *rope,
-                                        uint32_t layer, uint32_t pos)
+                                        const float *bias, uint32_t layer, uint32_t pos)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
@@ -649,6 +650,10 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
     for (uint32_t rl = 2 * tid(); rl < hi - lo; rl += 2 * MK_THREADS) {
         const uint32_t r = lo + rl;
         float v0 = row_sum<1>(part, rl, 0, ns), v1 = row_sum<1>(part, rl + 1, 0, ns);
+        if (bias) {
+            v0 += bias[r];
+            v1 += bias[r + 1];
+        }
         if (r < nq + kvd) {
             const uint32_t i = ((r < nq ? r : r - nq) % hd) / 2;
             const float c = rope[i], s = rope[half + i];
@@ -1214,7 +1219,10 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 else gemv<TL, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
-                if (kind == MK_QKV) epi_qkv(a, g, part, rope, layer, pos);
+                if (kind == MK_QKV)
+                    epi_qkv(a, g, part, rope,
+                            a.bqkv ? a.bqkv + (size_t)layer * (a.n_embd + 2 * a.n_kv * a.head_dim) : nullptr,
+                            layer, pos);
                 else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out);
                 else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
                 else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd, tag_out);

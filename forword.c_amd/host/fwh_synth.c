@@ -344,7 +344,7 @@ size_t fwh_quantize(uint32_t t, const float *src, size_t n, void *dst)
 /* ── GGUF image writer ───────────────────────────────────────────────────── */
 
 enum { T_EMBD = 0, T_ATTN_NORM, T_Q, T_K, T_V, T_O, T_FFN_NORM, T_GATE, T_UP, T_DOWN,
-       T_OUT_NORM, T_OUT };
+       T_OUT_NORM, T_OUT, T_BIAS };
 
 typedef struct {
     char     name[64];
@@ -393,7 +393,7 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         s->n_embd % fwh_block_values(s->output_type))
         return -1;
     uint64_t hd = s->n_embd / s->n_head, kvd = hd * s->n_head_kv;
-    L->t = (tdesc_t *)calloc(9 * (size_t)s->n_layer + 3, sizeof(tdesc_t));
+    L->t = (tdesc_t *)calloc(12 * (size_t)s->n_layer + 3, sizeof(tdesc_t));
     if (!L->t) return -1;
     char nm[64];
     add_t(L, "token_embd.weight", T_EMBD, s->embd_type, s->n_embd, s->n_vocab, 2);
@@ -402,6 +402,11 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, s->n_embd, 2);
         snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); add_t(L, nm, T_K, s->linear_type, s->n_embd, kvd, 2);
         snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, s->linear_type, s->n_embd, kvd, 2);
+        if (s->qkv_bias) {
+            snprintf(nm, sizeof nm, "blk.%u.attn_q.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1);
+            snprintf(nm, sizeof nm, "blk.%u.attn_k.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
+            snprintf(nm, sizeof nm, "blk.%u.attn_v.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
+        }
         snprintf(nm, sizeof nm, "blk.%u.attn_output.weight", l); add_t(L, nm, T_O, s->linear_type, s->n_embd, s->n_embd, 2);
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l); add_t(L, nm, T_FFN_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
         snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); add_t(L, nm, T_GATE, s->linear_type, s->n_embd, s->n_ff, 2);
@@ -411,16 +416,17 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
     add_t(L, "output_norm.weight", T_OUT_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
     add_t(L, "output.weight", T_OUT, s->output_type, s->n_embd, s->n_vocab, 2);
 
-    /* metadata: 8 llama keys + architecture + name + tokenizer model + tokens */
+    /* metadata: 8 <arch> keys + architecture + name + tokenizer model + tokens */
+    const char *arch = s->qkv_bias ? "qwen2" : "llama";
+    const size_t arch_len = strlen(arch), pre = arch_len + 1;            /* "<arch>." prefix */
     size_t m = 0;
-    m += str_bytes(strlen("general.architecture")) + 4 + str_bytes(5);
+    m += str_bytes(strlen("general.architecture")) + 4 + str_bytes(arch_len);
     m += str_bytes(strlen("general.name")) + 4 + str_bytes(strlen("forword-synth"));
-    static const char *u32keys[] = { "llama.embedding_length", "llama.block_count",
-        "llama.attention.head_count", "llama.attention.head_count_kv", "llama.feed_forward_length",
-        "llama.context_length" };
-    for (int i = 0; i < 6; i++) m += str_bytes(strlen(u32keys[i])) + 4 + 4;
-    m += str_bytes(strlen("llama.rope.freq_base")) + 4 + 4;
-    m += str_bytes(strlen("llama.attention.layer_norm_rms_epsilon")) + 4 + 4;
+    static const char *u32keys[] = { "embedding_length", "block_count", "attention.head_count",
+        "attention.head_count_kv", "feed_forward_length", "context_length" };
+    for (int i = 0; i < 6; i++) m += str_bytes(pre + strlen(u32keys[i])) + 4 + 4;
+    m += str_bytes(pre + strlen("rope.freq_base")) + 4 + 4;
+    m += str_bytes(pre + strlen("attention.layer_norm_rms_epsilon")) + 4 + 4;
     m += str_bytes(strlen("tokenizer.ggml.model")) + 4 + str_bytes(5);
     m += str_bytes(strlen("tokenizer.ggml.tokens")) + 4 + 4 + 8;
     char tb[32];
@@ -449,6 +455,13 @@ static void w_f32(wr_t *w, float v) { w_bytes(w, &v, 4); }
 static void w_str(wr_t *w, const char *s, size_t n) { w_u64(w, n); w_bytes(w, s, n); }
 static void w_cstr(wr_t *w, const char *s) { w_str(w, s, strlen(s)); }
 
+/* "<arch>.<suffix>" metadata key (model_config.c:53-57 builds the same names). */
+static const char *arch_key(char *buf, size_t n, const char *arch, const char *suffix)
+{
+    snprintf(buf, n, "%s.%s", arch, suffix);
+    return buf;
+}
+
 typedef struct {
     const layout_t *L;
     uint8_t *data;          /* start of data section */
@@ -471,7 +484,8 @@ static void gen_job(void *vctx, size_t job)
     uint64_t row_bytes = t->bytes / t->rows;
     for (size_t r = r0; r < r1; r++) {
         int is_norm = t->kind == T_ATTN_NORM || t->kind == T_FFN_NORM || t->kind == T_OUT_NORM;
-        fwh_randn(row_seed(tseed, r), is_norm ? L->s.norm_std : L->s.w_std, buf, t->cols);
+        fwh_randn(row_seed(tseed, r), is_norm ? L->s.norm_std : t->kind == T_BIAS ? 4.0f * L->s.w_std : L->s.w_std,
+                  buf, t->cols);
         if (is_norm) for (size_t j = 0; j < t->cols; j++) buf[j] += 1.0f;
         fwh_quantize(t->type, buf, t->cols, c->data + t->offset + r * row_bytes);
     }
@@ -497,16 +511,20 @@ size_t fwh_synth_write(const fwh_synth_spec_t *spec, void *out, size_t cap)
     w_u32(&w, 3);
     w_u64(&w, L.n_t);
     w_u64(&w, 12);
-    w_cstr(&w, "general.architecture"); w_u32(&w, 8); w_cstr(&w, "llama");
+    const char *arch = s->qkv_bias ? "qwen2" : "llama";
+    char key[96];
+#define ARCH_KEY(k) arch_key(key, sizeof key, arch, k)
+    w_cstr(&w, "general.architecture"); w_u32(&w, 8); w_cstr(&w, arch);
     w_cstr(&w, "general.name"); w_u32(&w, 8); w_cstr(&w, "forword-synth");
-    w_cstr(&w, "llama.embedding_length"); w_u32(&w, 4); w_u32(&w, s->n_embd);
-    w_cstr(&w, "llama.block_count"); w_u32(&w, 4); w_u32(&w, s->n_layer);
-    w_cstr(&w, "llama.attention.head_count"); w_u32(&w, 4); w_u32(&w, s->n_head);
-    w_cstr(&w, "llama.attention.head_count_kv"); w_u32(&w, 4); w_u32(&w, s->n_head_kv);
-    w_cstr(&w, "llama.feed_forward_length"); w_u32(&w, 4); w_u32(&w, s->n_ff);
-    w_cstr(&w, "llama.context_length"); w_u32(&w, 4); w_u32(&w, s->n_ctx);
-    w_cstr(&w, "llama.rope.freq_base"); w_u32(&w, 6); w_f32(&w, s->rope_freq_base);
-    w_cstr(&w, "llama.attention.layer_norm_rms_epsilon"); w_u32(&w, 6); w_f32(&w, s->norm_eps);
+    w_cstr(&w, ARCH_KEY("embedding_length")); w_u32(&w, 4); w_u32(&w, s->n_embd);
+    w_cstr(&w, ARCH_KEY("block_count")); w_u32(&w, 4); w_u32(&w, s->n_layer);
+    w_cstr(&w, ARCH_KEY("attention.head_count")); w_u32(&w, 4); w_u32(&w, s->n_head);
+    w_cstr(&w, ARCH_KEY("attention.head_count_kv")); w_u32(&w, 4); w_u32(&w, s->n_head_kv);
+    w_cstr(&w, ARCH_KEY("feed_forward_length")); w_u32(&w, 4); w_u32(&w, s->n_ff);
+    w_cstr(&w, ARCH_KEY("context_length")); w_u32(&w, 4); w_u32(&w, s->n_ctx);
+    w_cstr(&w, ARCH_KEY("rope.freq_base")); w_u32(&w, 6); w_f32(&w, s->rope_freq_base);
+    w_cstr(&w, ARCH_KEY("attention.layer_norm_rms_epsilon")); w_u32(&w, 6); w_f32(&w, s->norm_eps);
+#undef ARCH_KEY
     w_cstr(&w, "tokenizer.ggml.model"); w_u32(&w, 8); w_cstr(&w, "llama");
     w_cstr(&w, "tokenizer.ggml.tokens"); w_u32(&w, 9); w_u32(&w, 8); w_u64(&w, s->n_vocab);
     char tb[32];

@@ -440,6 +440,7 @@ struct fwc_model {
     const float *out_norm;
     struct layer {
         const float *attn_norm, *ffn_norm;
+        const float *bq, *bk, *bv, *bo;    /* F32 biases, null when absent */
         lin_t q, k, v, o, gate, up, down;
     } *L;
     const float *cos_tab, *sin_tab;
@@ -488,7 +489,7 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
     if (!data || !t || !cfg || !max_ctx || !cos_tab || !sin_tab) return NULL;
     const forword_gpu_config_t *c = cfg;
     if (c->norm_type != FORWORD_NORM_RMS || !c->use_ffn_gate || c->act_type != FORWORD_ACT_SILU ||
-        c->use_qkv_bias || c->parallel_res || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
+        c->parallel_res || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
         c->n_head % c->n_head_kv || c->head_dim % 2 || c->n_embd != c->n_head * c->head_dim) {
         fprintf(stderr, "fwc_model_init: unsupported model variant\n");
         return NULL;
@@ -522,6 +523,16 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
         L->attn_norm = bind_vec(m, find(t, nt, nm), c->n_embd);
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);
         L->ffn_norm = bind_vec(m, find(t, nt, nm), c->n_embd);
+        /* attention.c:106-122: attn_output.bias whenever present, q/k/v biases
+         * when the architecture has them; linear.c:214-221 adds F32 biases only. */
+        const size_t kvd = (size_t)c->n_head_kv * c->head_dim;
+        snprintf(nm, sizeof nm, "blk.%u.attn_output.bias", l);
+        L->bo = bind_vec(m, find(t, nt, nm), c->n_embd);
+        if (c->use_qkv_bias) {
+            snprintf(nm, sizeof nm, "blk.%u.attn_q.bias", l); L->bq = bind_vec(m, find(t, nt, nm), c->n_embd);
+            snprintf(nm, sizeof nm, "blk.%u.attn_k.bias", l); L->bk = bind_vec(m, find(t, nt, nm), kvd);
+            snprintf(nm, sizeof nm, "blk.%u.attn_v.bias", l); L->bv = bind_vec(m, find(t, nt, nm), kvd);
+        }
     }
     size_t kvd = (size_t)c->n_head_kv * c->head_dim, kvn = (size_t)c->n_layer * max_ctx * kvd;
     m->kv_k = calloc(kvn, 4); m->kv_v = calloc(kvn, 4);
@@ -555,6 +566,11 @@ static int get_row(const lin_t *l, size_t row, float *out)
     return fwc_dequant(l->p + row * rb, rb, l->type, out, l->in);
 }
 
+static void add_bias(float *y, const float *b, size_t n)
+{
+    if (b) for (size_t i = 0; i < n; i++) y[i] += b[i];
+}
+
 float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
 {
     const forword_gpu_config_t *c = &m->c;
@@ -568,6 +584,9 @@ float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
         fwc_rms_norm(m->x, L->attn_norm, m->xn, n, c->norm_eps);
         /* attention_forward (attention.c:124-166) */
         if (lin(&L->q, m->xn, m->q) || lin(&L->k, m->xn, m->k) || lin(&L->v, m->xn, m->v)) return NULL;
+        add_bias(m->q, L->bq, n);                                /* linear.c:214-221 */
+        add_bias(m->k, L->bk, kvd);
+        add_bias(m->v, L->bv, kvd);
         fwc_rope_apply(m->q, pos, c->n_head, hd, m->cos_tab, m->sin_tab, neox);
         fwc_rope_apply(m->k, pos, c->n_head_kv, hd, m->cos_tab, m->sin_tab, neox);
         memcpy(fwc_kv_k(m, l, pos), m->k, kvd * 4);
@@ -575,6 +594,7 @@ float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
         fwc_attention_core(m->q, fwc_kv_k(m, l, 0), fwc_kv_v(m, l, 0), m->att, c->n_head,
                            c->n_head_kv, hd, pos, m->scores);
         if (lin(&L->o, m->att, m->attn_out)) return NULL;
+        add_bias(m->attn_out, L->bo, n);
         for (size_t i = 0; i < n; i++) m->x[i] += m->attn_out[i];
         memcpy(m->trace + (2 * (size_t)l) * n, m->x, n * 4);
         fwc_rms_norm(m->x, L->ffn_norm, m->xn, n, c->norm_eps);

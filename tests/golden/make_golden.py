@@ -188,8 +188,11 @@ def main():
         with open(os.path.join(GOLD, "manifest.json")) as f:
             manifest = json.load(f)
         with tempfile.TemporaryDirectory() as tmp:
-            {"kquant": gen_kquant, "sampler": gen_sampler, "matvec": gen_matvec, "dequant": gen_dequant,
-             "ops": gen_ops}[only](tmp, manifest)
+            if only.startswith("model:"):      # --only model:<name>
+                gen_model(only[6:], tmp, manifest)
+            else:
+                {"kquant": gen_kquant, "sampler": gen_sampler, "matvec": gen_matvec, "dequant": gen_dequant,
+                 "ops": gen_ops}[only](tmp, manifest)
         with open(os.path.join(GOLD, "manifest.json"), "w") as f:
             json.dump(manifest, f, indent=1, sort_keys=True)
         print("fixture", only, "written to", GOLD)

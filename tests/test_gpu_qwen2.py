@@ -1,0 +1,109 @@
+"""The qwen2 block on the GPU: llama's block plus F32 biases on the q, k and v
+projections (attention.c:114-126 via linear.c:214-221), added before RoPE, and
+the RoPE base the config loader raises to 1e6 (model_config.c:161-168).
+
+Every decode path adds the bias in its own epilogue: the persistent step
+kernel, the per-phase kernels (fused QKV launch, and separate launches when
+q/k/v types differ) and the batched prefill.  Each is held to the oracle, whose
+qwen2 forward is pinned bit-exactly to the reference by the "qwen2" golden
+fixture.  Bar: logits and the residual stream within max-abs 2e-3 / rel 1e-3,
+identical greedy tokens."""
+import os
+
+import numpy as np
+import pytest
+
+import fw_cpu
+import fwgpu
+import golden_specs as gs
+from conftest import gold_model
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 2e-3, 1e-3
+Q4, Q8 = fwgpu.GGML_Q4_0, fwgpu.GGML_Q8_0
+
+
+def close(got, exp, what):
+    err = np.abs(got.astype(np.float64) - exp.astype(np.float64))
+    bad = err > ATOL + RTOL * np.abs(exp)
+    assert not bad.any(), f"{what}: {bad.sum()} elements out of tolerance, max err {err.max():.3g}"
+    return float(err.max())
+
+
+class env:
+    def __init__(self, **kw):
+        self.kw = kw
+
+    def __enter__(self):
+        for k, v in self.kw.items():
+            os.environ[k] = v
+
+    def __exit__(self, *a):
+        for k in self.kw:
+            del os.environ[k]
+
+
+def qwen2_q4(seed=21):
+    # head_dim 64, GQA group 4, Q4_0 layers (the persistent kernel's shape class)
+    return fwgpu.spec(512, 1536, 2, 8, 2, 2048, 96, 10000.0, linear_type=Q4, seed=seed, qkv_bias=True)
+
+
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_phase"])
+def test_qwen2_decode_matches_oracle(persistent):
+    fw_cpu.set_threads(8)
+    with env(**({} if persistent else {"FORWORD_GPU_MEGAKERNEL": "0"})):
+        with fwgpu.HostModel(synth=qwen2_q4()) as host, fwgpu.GpuModel(host) as gm, \
+                fw_cpu.OracleModel(host) as om:
+            assert host.cfg.use_qkv_bias == 1 and host.cfg.rope_freq_base == 1e6
+            assert gm.persistent == persistent
+            toks = np.random.default_rng(4).integers(3, host.cfg.n_vocab, 10)
+            for pos, t in enumerate(toks):
+                lg, ref = gm.forward(int(t), pos), om.forward(int(t), pos)
+                close(lg, ref, f"logits at position {pos}")
+                assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+                if pos in (0, 9):
+                    close(gm.layer_trace().reshape(-1), om.trace().reshape(-1), f"residual stream at {pos}")
+            k, v = gm.kv_read(host.cfg.n_layer - 1, 0, len(toks))
+            kr, vr = om.kv(host.cfg.n_layer - 1, 0)
+            close(k[0], kr, "post-RoPE K row (bias before RoPE)")
+            close(v[0], vr, "V row (bias)")
+
+
+def test_qwen2_fixture_per_phase_matches_reference():
+    """The reference-generated qwen2 fixture on the per-phase kernels (the
+    model-level tests run it on the persistent kernel): logits at the recorded
+    forwards and the greedy continuation."""
+    prompt = gs.prompt("qwen2")
+    gold = gold_model("qwen2")
+    m = gs.MODELS["qwen2"]
+    with env(FORWORD_GPU_MEGAKERNEL="0"):
+        with fwgpu.HostModel(synth=m["spec"](), max_ctx=m["max_ctx"]) as host, fwgpu.GpuModel(host) as gm:
+            assert not gm.persistent
+            toks = gold["tokens"]
+            for f in range(gs.n_forwards("qwen2")):
+                lg = gm.forward(int(toks[f]), f)
+                assert fw_cpu.argmax(lg) == int(gold["stats"][f, 0]), f"greedy choice differs at forward {f}"
+                if f in gs.logit_steps("qwen2"):
+                    close(lg, gold[f"logits_{f}"], f"logits at forward {f}")
+            got = gm.generate_greedy(prompt, m["n_gen"])
+    assert np.array_equal(got, gold["tokens"][len(prompt):])
+
+
+def test_qwen2_prefill_matches_oracle():
+    """Batched prefill adds the bias in its RoPE/append kernel: last-token
+    logits and every KV row against the oracle's token-by-token prefill."""
+    fw_cpu.set_threads(8)
+    with fwgpu.HostModel(synth=qwen2_q4(seed=22)) as host, fwgpu.GpuModel(host) as gm, \
+            fw_cpu.OracleModel(host) as om:
+        prompt = np.random.default_rng(6).integers(3, host.cfg.n_vocab, 40).astype(np.uint32)
+        lg = gm.prefill(prompt)
+        for pos, t in enumerate(prompt):
+            ref = om.forward(int(t), pos)
+        close(lg, ref, "prefill logits")
+        assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+        for layer in range(host.cfg.n_layer):
+            k, v = gm.kv_read(layer, 0, len(prompt))
+            for pos in (0, 17, len(prompt) - 1):
+                kr, vr = om.kv(layer, pos)
+                close(k[pos], kr, f"K row layer {layer} pos {pos}")
+                close(v[pos], vr, f"V row layer {layer} pos {pos}")
