@@ -349,4 +349,21 @@ __device__ __forceinline__ float silu_ref(float v)
     return v * sig;
 }
 
+// The gated FFN's GELU forms: erf (ffn.c:27-31) and tanh (ffn.c:33-42).
+__device__ __forceinline__ float gelu_erf(float v)
+{
+    return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+}
+
+__device__ __forceinline__ float gelu_tanh(float v)
+{
+    const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);   // sqrt(2/pi) (v + 0.044715 v^3)
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+__device__ __forceinline__ float ffn_act(float v, uint32_t act)
+{
+    return act == ACT_GELU ? gelu_erf(v) : act == ACT_GELU_TANH ? gelu_tanh(v) : silu_ref(v);
+}
+
 } // namespace fw

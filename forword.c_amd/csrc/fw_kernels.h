@@ -23,6 +23,10 @@ struct StepState {
 
 enum Epi : int { EPI_STORE = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
 
+// Activation codes of the gated FFN (ffn.c:88-101): silu (also the default for
+// any other code), gelu with erf (ffn.c:27-31), gelu with tanh (ffn.c:33-42).
+enum FfnAct : uint32_t { ACT_SILU = 0, ACT_GELU = 1, ACT_GELU_TANH = 2 };
+
 // One GEMV launch over up to three weight matrices that share the input x and
 // the column count (fused QKV; gate+up).  Rows of matrix s are rows[s].
 struct QmvArgs {
@@ -54,6 +58,7 @@ struct QmvArgs {
     uint32_t *ticket;
     float *scale_out;
     float norm_eps;
+    uint32_t act;              // SWIGLU: FfnAct of the gate (silu / gelu / gelu-tanh)
 };
 
 // Rows computed by one wave of the GEMV kernels.
@@ -94,6 +99,8 @@ uint32_t argmax_blocks(uint32_t n);
 hipError_t launch_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t head_dim, const float *cos_tab,
                        const float *sin_tab, int neox, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s);
+// out = act(g) * u with an FfnAct code (ffn.c:88-104).
+hipError_t launch_act_mul(const float *g, const float *u, float *out, uint64_t n, uint32_t act, hipStream_t s);
 hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);
 

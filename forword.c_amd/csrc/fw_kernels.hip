@@ -265,7 +265,7 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
         if (lane == 0)
 #pragma unroll
             for (int k = 0; k < R / 2; k++)
-                if (ok[k]) a.out[0][row[k]] = silu_ref(acc[k]) * acc[k + R / 2];   // ffn.c:88-104
+                if (ok[k]) a.out[0][row[k]] = ffn_act(acc[k], a.act) * acc[k + R / 2];   // ffn.c:88-104
     } else {   // EPI_QKV: bias (linear.c:214-221), RoPE on q and k rows (rope.c:37-43), q out / KV append at pos
         if (lane == 0 && active) {
             const uint32_t pos = a.state->pos, half = a.head_dim / 2;
@@ -790,6 +790,12 @@ __global__ void k_silu_mul(const float *g, const float *u, float *out, uint64_t 
         out[i] = silu_ref(g[i]) * u[i];
 }
 
+__global__ void k_act_mul(const float *g, const float *u, float *out, uint64_t n, uint32_t act)
+{
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = ffn_act(g[i], act) * u[i];
+}
+
 __global__ void k_silu(const float *x, float *out, uint64_t n)
 {
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
@@ -811,6 +817,12 @@ static uint32_t ew_blocks(uint64_t n)
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s)
 {
     hipLaunchKernelGGL(k_silu_mul, dim3(ew_blocks(n)), dim3(256), 0, s, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_act_mul(const float *g, const float *u, float *out, uint64_t n, uint32_t act, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_act_mul, dim3(ew_blocks(n)), dim3(256), 0, s, g, u, out, n, act);
     return hipGetLastError();
 }
 

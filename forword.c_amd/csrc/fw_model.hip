@@ -78,6 +78,15 @@ uint64_t type_row_bytes(uint32_t type, uint64_t cols)
     }
 }
 
+// The gated FFN's activation (ffn.c:88-101): GELU and GELU-tanh by their codes,
+// silu for silu and for every other code (the switch's default).
+static uint32_t ffn_act_code(const forword_gpu_config_t &c)
+{
+    return c.act_type == FORWORD_ACT_GELU        ? fw::ACT_GELU
+         : c.act_type == FORWORD_ACT_GELU_FAST ? fw::ACT_GELU_TANH
+                                               : fw::ACT_SILU;
+}
+
 // Values per block of a block type (gguf.c:211-223); 1 for F32, 0 unknown.
 uint32_t type_block_values(uint32_t type)
 {
@@ -257,6 +266,7 @@ static hipError_t enqueue_step(forword_gpu_t *h)
             a.n_seg = 2; a.w[0] = Ly.gate.w; a.w[1] = Ly.up.w; a.rows[0] = a.rows[1] = c.n_ff;
             a.n_cols = n; a.row_bytes = Ly.gate.row_bytes; a.x = h->d_x; a.out[0] = h->d_h;
             a.norm_w = Ly.ffn_norm; a.norm_scale = h->d_scale;
+            a.act = ffn_act_code(c);
             qmv_plan(a, EPI_SWIGLU);
             TRY(launch_qmv(Ly.gate.type, EPI_SWIGLU, a, s));
         }
@@ -361,6 +371,7 @@ static int setup_mk(forword_gpu_t *h)
     a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
     a.kc = h->d_k; a.vc = h->d_v; a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
     a.bqkv = h->d_bias;
+    a.act = ffn_act_code(c);
     a.q = h->d_q; a.logits = h->d_logits; a.trace = h->d_trace;
     a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
     // (KV head, split) attention items: about one per workgroup, >= 8 positions per split
@@ -479,9 +490,8 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         set_err("forword_gpu_init: invalid model dimensions");
         return -1;
     }
-    if (c.norm_type != FORWORD_NORM_RMS || c.act_type != FORWORD_ACT_SILU || !c.use_ffn_gate ||
-        c.parallel_res || c.rope_type != FORWORD_ROPE_NORMAL) {
-        set_err("forword_gpu_init: only the llama/qwen2 block (RMSNorm, SwiGLU, RoPE pairs (2i,2i+1), "
+    if (c.norm_type != FORWORD_NORM_RMS || !c.use_ffn_gate || c.parallel_res || c.rope_type != FORWORD_ROPE_NORMAL) {
+        set_err("forword_gpu_init: only the llama/qwen2/gemma block (RMSNorm, gated FFN, RoPE pairs (2i,2i+1), "
                 "sequential residual) is implemented");
         return -1;
     }
@@ -789,7 +799,7 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
             TRY(launch_rmsnorm_rows(X, Ly.ffn_norm, Xn, n, rows, c.norm_eps, s));             // :275
             TRY(launch_gemm_q(Ly.gate.type, Xn, n, Ly.gate.w, Ly.gate.row_bytes, G, nff, rows, nff, n, false, s));
             TRY(launch_gemm_q(Ly.up.type, Xn, n, Ly.up.w, Ly.up.row_bytes, U, nff, rows, nff, n, false, s));
-            TRY(launch_silu_mul(G, U, G, (uint64_t)rows * nff, s));                           // ffn.c:95-103
+            TRY(launch_act_mul(G, U, G, (uint64_t)rows * nff, ffn_act_code(c), s));           // ffn.c:88-103
             TRY(launch_gemm_q(Ly.down.type, G, nff, Ly.down.w, Ly.down.row_bytes, X, n, rows, n, nff, true, s));
         }
     }

@@ -43,6 +43,7 @@ struct MkArgs {
     uint64_t embd_row_bytes;
     float embd_scale;
     uint32_t n_embd, n_ff, n_head, n_kv, head_dim, n_vocab, n_ctx, n_splits;
+    uint32_t act;            // FfnAct of the gated FFN
     float eps;
     float *kc, *vc;
     const float *cos_tab, *sin_tab;

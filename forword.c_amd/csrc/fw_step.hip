@@ -698,14 +698,17 @@ __device__ __forceinline__ float silu_f(float v)
     return v * sig;
 }
 
-// h = silu(gate x) * (up x) (ffn.c:82-104).
+// h = act(gate x) * (up x) (ffn.c:82-104): silu, or a GELU form.
 __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part, uint32_t tag)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices(g.n_cols);
-    for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS)
-        st_sys64(a.th + lo + rl, tagged(silu_f(row_sum<2>(part, rl, 0, ns)) * row_sum<2>(part, rl, 1, ns), tag));
+    for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
+        const float gv = row_sum<2>(part, rl, 0, ns);
+        const float av = a.act == ACT_SILU ? silu_f(gv) : a.act == ACT_GELU ? gelu_erf(gv) : gelu_tanh(gv);
+        st_sys64(a.th + lo + rl, tagged(av * row_sum<2>(part, rl, 1, ns), tag));
+    }
 }
 
 __device__ __forceinline__ bool am_better_mk(float v1, uint32_t i1, float v2, uint32_t i2)

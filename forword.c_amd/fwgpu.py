@@ -30,6 +30,8 @@ GPU_LIB = os.path.join(LIBDIR, "libforword_gpu.so")
 GGML_F32, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 2, 6, 8, 12, 14
 BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q5_0: 22, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
 BLOCK_VALUES = {GGML_Q4_0: 32, GGML_Q5_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
+# Architectures the synthetic writer emits, as FORWORD_ARCH_* values (model_config.h:12-24).
+SYNTH_ARCHS = {"llama": 2, "qwen2": 3, "gemma": 5}
 TYPE_NAMES = {GGML_F32: "F32", GGML_Q4_0: "Q4_0", GGML_Q5_0: "Q5_0", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K",
               GGML_Q6_K: "Q6_K"}
 
@@ -59,16 +61,17 @@ class SynthSpec(C.Structure):
     _fields_ = [("n_embd", u32), ("n_ff", u32), ("n_layer", u32), ("n_head", u32), ("n_head_kv", u32),
                 ("n_vocab", u32), ("n_ctx", u32), ("rope_freq_base", f32), ("norm_eps", f32),
                 ("linear_type", u32), ("embd_type", u32), ("output_type", u32), ("seed", u64),
-                ("w_std", f32), ("norm_std", f32), ("threads", u32), ("qkv_bias", u32)]
+                ("w_std", f32), ("norm_std", f32), ("threads", u32), ("arch", u32)]
 
 
 def spec(n_embd, n_ff, n_layer, n_head, n_head_kv, n_vocab, n_ctx, rope_freq_base=10000.0,
          norm_eps=1e-5, linear_type=GGML_Q8_0, embd_type=GGML_Q8_0, output_type=GGML_Q8_0,
-         seed=1, w_std=0.02, norm_std=0.01, threads=0, qkv_bias=False) -> SynthSpec:
-    """Synthetic model shape; qkv_bias=True writes a qwen2 model (attn_{q,k,v}.bias per layer)."""
+         seed=1, w_std=0.02, norm_std=0.01, threads=0, arch="llama") -> SynthSpec:
+    """Synthetic model shape.  arch "qwen2" adds attn_{q,k,v}.bias per layer; "gemma"
+    (gated GELU-tanh FFN, embedding times sqrt(n_embd)) ties the lm-head to token_embd."""
     return SynthSpec(n_embd, n_ff, n_layer, n_head, n_head_kv, n_vocab, n_ctx, rope_freq_base,
                      norm_eps, linear_type, embd_type, output_type, seed, w_std, norm_std, threads,
-                     1 if qkv_bias else 0)
+                     SYNTH_ARCHS[arch])
 
 
 # Workload shapes (dims, heads, ffn, vocab, RoPE base) of the configurations this path is measured on.

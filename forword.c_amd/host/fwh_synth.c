@@ -381,6 +381,12 @@ static size_t str_bytes(size_t len) { return 8 + len; }
 
 static int token_text(uint32_t i, char *buf) { return sprintf(buf, "<t%u>", i); }
 
+/* Architectures the writer emits (model_config.c:10-22 names). */
+static const char *synth_arch_name(uint32_t arch)
+{
+    return arch == FORWORD_ARCH_QWEN2 ? "qwen2" : arch == FORWORD_ARCH_GEMMA ? "gemma" : "llama";
+}
+
 static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
 {
     memset(L, 0, sizeof *L);
@@ -402,7 +408,7 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, s->n_embd, 2);
         snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); add_t(L, nm, T_K, s->linear_type, s->n_embd, kvd, 2);
         snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, s->linear_type, s->n_embd, kvd, 2);
-        if (s->qkv_bias) {
+        if (s->arch == FORWORD_ARCH_QWEN2) {
             snprintf(nm, sizeof nm, "blk.%u.attn_q.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1);
             snprintf(nm, sizeof nm, "blk.%u.attn_k.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
             snprintf(nm, sizeof nm, "blk.%u.attn_v.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
@@ -414,10 +420,11 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); add_t(L, nm, T_DOWN, s->linear_type, s->n_ff, s->n_embd, 2);
     }
     add_t(L, "output_norm.weight", T_OUT_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
-    add_t(L, "output.weight", T_OUT, s->output_type, s->n_embd, s->n_vocab, 2);
+    if (s->arch != FORWORD_ARCH_GEMMA)
+        add_t(L, "output.weight", T_OUT, s->output_type, s->n_embd, s->n_vocab, 2);
 
     /* metadata: 8 <arch> keys + architecture + name + tokenizer model + tokens */
-    const char *arch = s->qkv_bias ? "qwen2" : "llama";
+    const char *arch = synth_arch_name(s->arch);
     const size_t arch_len = strlen(arch), pre = arch_len + 1;            /* "<arch>." prefix */
     size_t m = 0;
     m += str_bytes(strlen("general.architecture")) + 4 + str_bytes(arch_len);
@@ -511,7 +518,7 @@ size_t fwh_synth_write(const fwh_synth_spec_t *spec, void *out, size_t cap)
     w_u32(&w, 3);
     w_u64(&w, L.n_t);
     w_u64(&w, 12);
-    const char *arch = s->qkv_bias ? "qwen2" : "llama";
+    const char *arch = synth_arch_name(s->arch);
     char key[96];
 #define ARCH_KEY(k) arch_key(key, sizeof key, arch, k)
     w_cstr(&w, "general.architecture"); w_u32(&w, 8); w_cstr(&w, arch);

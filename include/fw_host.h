@@ -96,8 +96,9 @@ typedef struct {
     float    w_std;               /* linear/embedding weights N(0, w_std) before quantisation */
     float    norm_std;            /* norm weights 1 + N(0, norm_std), F32 */
     uint32_t threads;             /* 0 = default */
-    uint32_t qkv_bias;            /* 1: architecture qwen2 (keys qwen2.*), F32 biases
-                                     blk.N.attn_{q,k,v}.bias ~ N(0, 4*w_std) */
+    uint32_t arch;                /* FORWORD_ARCH_*: 0 or LLAMA = llama; QWEN2 adds F32
+                                     blk.N.attn_{q,k,v}.bias ~ N(0, 4*w_std); GEMMA writes
+                                     no output.weight (the head reuses token_embd) */
 } fwh_synth_spec_t;
 
 /* Exact byte size of the GGUF image fwh_synth_write would produce. */

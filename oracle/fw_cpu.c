@@ -373,6 +373,23 @@ void fwc_silu(float *x, size_t n)
     }
 }
 
+/* apply_gelu (ffn.c:27-31): 0.5 v (1 + erf(v / sqrt 2)), libm erff. */
+void fwc_gelu(float *x, size_t n)
+{
+    const float inv_sqrt2 = 0.7071067811865476f;
+    for (size_t i = 0; i < n; i++) x[i] = 0.5f * x[i] * (1.0f + erff(x[i] * inv_sqrt2));
+}
+
+/* apply_gelu_fast (ffn.c:33-42): the tanh form, sqrt(2/pi) (v + 0.044715 v^3). */
+void fwc_gelu_fast(float *x, size_t n)
+{
+    const float c1 = 0.7978845608028654f, c2 = 0.044715f;
+    for (size_t i = 0; i < n; i++) {
+        const float v = x[i], inner = c1 * (v + c2 * v * v * v);
+        x[i] = 0.5f * v * (1.0f + tanhf(inner));
+    }
+}
+
 /* sampler_argmax (sampler.c:28-32). */
 uint32_t fwc_argmax(const float *x, size_t n)
 {
@@ -488,7 +505,7 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
 {
     if (!data || !t || !cfg || !max_ctx || !cos_tab || !sin_tab) return NULL;
     const forword_gpu_config_t *c = cfg;
-    if (c->norm_type != FORWORD_NORM_RMS || !c->use_ffn_gate || c->act_type != FORWORD_ACT_SILU ||
+    if (c->norm_type != FORWORD_NORM_RMS || !c->use_ffn_gate ||
         c->parallel_res || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
         c->n_head % c->n_head_kv || c->head_dim % 2 || c->n_embd != c->n_head * c->head_dim) {
         fprintf(stderr, "fwc_model_init: unsupported model variant\n");
@@ -600,7 +617,9 @@ float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
         fwc_rms_norm(m->x, L->ffn_norm, m->xn, n, c->norm_eps);
         /* ffn_forward gated branch (ffn.c:68-107) */
         if (lin(&L->gate, m->xn, m->gate) || lin(&L->up, m->xn, m->upb)) return NULL;
-        fwc_silu(m->gate, c->n_ff);
+        if (c->act_type == FORWORD_ACT_GELU) fwc_gelu(m->gate, c->n_ff);       /* ffn.c:88-101 */
+        else if (c->act_type == FORWORD_ACT_GELU_FAST) fwc_gelu_fast(m->gate, c->n_ff);
+        else fwc_silu(m->gate, c->n_ff);                                        /* silu, also the default */
         for (size_t i = 0; i < c->n_ff; i++) m->gate[i] *= m->upb[i];
         if (lin(&L->down, m->gate, m->ffn_out)) return NULL;
         for (size_t i = 0; i < n; i++) m->x[i] += m->ffn_out[i];

@@ -46,6 +46,8 @@ void     fwc_rope_apply(float *qk, size_t pos, size_t n_heads, size_t hd, const 
                         const float *sin_tab, int neox);
 void     fwc_softmax(float *x, size_t n);
 void     fwc_silu(float *x, size_t n);
+void     fwc_gelu(float *x, size_t n);
+void     fwc_gelu_fast(float *x, size_t n);
 uint32_t fwc_argmax(const float *x, size_t n);
 /* attention core (attention.c:142-164) over one layer's KV slice */
 void     fwc_attention_core(const float *q, const float *kc, const float *vc, float *out,

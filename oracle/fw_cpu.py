@@ -35,6 +35,8 @@ def lib():
         s(L, "fwc_rope_apply", None, [fp, sz, sz, sz, fp, fp, C.c_int])
         s(L, "fwc_softmax", None, [fp, sz])
         s(L, "fwc_silu", None, [fp, sz])
+        s(L, "fwc_gelu", None, [fp, sz])
+        s(L, "fwc_gelu_fast", None, [fp, sz])
         s(L, "fwc_argmax", C.c_uint32, [fp, sz])
         s(L, "fwc_attention_core", None, [fp, fp, fp, fp, sz, sz, sz, sz, fp])
         s(L, "fwc_tensor_matvec_f32", C.c_int, [fp, fp, fp, sz, sz])
@@ -121,6 +123,18 @@ def softmax(x) -> np.ndarray:
 def silu(x) -> np.ndarray:
     x = np.array(x, np.float32, copy=True)
     lib().fwc_silu(_f(x), x.size)
+    return x
+
+
+def gelu(x) -> np.ndarray:
+    x = np.array(x, np.float32, copy=True)
+    lib().fwc_gelu(_f(x), x.size)
+    return x
+
+
+def gelu_fast(x) -> np.ndarray:
+    x = np.array(x, np.float32, copy=True)
+    lib().fwc_gelu_fast(_f(x), x.size)
     return x
 
 

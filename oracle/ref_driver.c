@@ -76,14 +76,16 @@ static int in_list(const char *list, size_t v)
     return 0;
 }
 
-/* transformer.c:149-326, llama branch (sequential residual, RMSNorm), with the
- * residual stream copied out after each residual add. */
+/* transformer.c:149-326, RMSNorm / sequential-residual branch (llama, qwen2,
+ * gemma), with the residual stream copied out after each residual add. */
 static float *traced_forward(transformer_t *t, uint32_t tok, size_t pos, float *trace)
 {
     const model_config_t *c = &t->cfg;
     const gguf_file_t *g = &t->g;
     const size_t n = c->n_embd;
     if (linear_get_row(g, tensor_find(g, "token_embd.weight"), tok, t->x)) return NULL;
+    if (c->embd_scale != 1.0f)                                      /* transformer.c:179-182 */
+        for (size_t i = 0; i < n; i++) t->x[i] *= c->embd_scale;
     for (size_t l = 0; l < c->n_layer; l++) {
         char nm[128];
         snprintf(nm, sizeof nm, "blk.%zu.attn_norm.weight", l);
@@ -102,7 +104,9 @@ static float *traced_forward(transformer_t *t, uint32_t tok, size_t pos, float *
     }
     const float *w = (const float *)tensor_data(g, tensor_find(g, "output_norm.weight"), NULL);
     rms_norm(t->x, w, t->xn, n, c->norm_eps);
-    const gguf_tensor_t *ow = tensor_find(g, "output.weight");
+    const gguf_tensor_t *ow = tensor_find(g, "output.weight");     /* transformer.c:309-316 */
+    if (!ow) ow = tensor_find(g, "lm_head.weight");
+    if (!ow) ow = tensor_find(g, "token_embd.weight");
     if (linear_forward(g, ow, NULL, t->xn, t->logits, NULL)) return NULL;
     return t->logits;
 }

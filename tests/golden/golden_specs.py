@@ -19,7 +19,8 @@ Q4K, Q6K = fwgpu.GGML_Q4_K, fwgpu.GGML_Q6_K
 # ctx 256, all Q8_0, theta 1e4, 16-token prompt + 128 greedy tokens.  "gqa":
 # 8 query / 2 KV heads (group 4).  "q5": Q5_0 linears, embedding and output.
 # "qwen2": architecture qwen2 (q/k/v biases, RoPE base raised to 1e6 by the
-# config loader), 8/2 heads, Q8_0 linears.
+# config loader), 8/2 heads, Q8_0 linears.  "gemma": gated FFN with the tanh
+# GELU, embedding rows times sqrt(n_embd), lm-head tied to token_embd.
 MODELS = {
     "tiny": {"spec": lambda: fwgpu.spec_tiny(seed=20240601), "n_prompt": 16, "n_gen": 128,
              "max_ctx": 0, "prompt_seed": 1},
@@ -29,8 +30,10 @@ MODELS = {
                                       embd_type=Q5, output_type=Q5, seed=55),
            "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 3},
     "qwen2": {"spec": lambda: fwgpu.spec(256, 512, 2, 8, 2, 1000, 64, 10000.0, seed=99,
-                                         qkv_bias=True),
+                                         arch="qwen2"),
               "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 4},
+    "gemma": {"spec": lambda: fwgpu.spec(256, 512, 2, 8, 2, 1000, 64, 10000.0, seed=123, arch="gemma"),
+              "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 5},
 }
 
 

@@ -70,7 +70,7 @@ def test_init_rejects_unsupported_variant():
                                               host.n_tensors, C.byref(cfg), host.n_ctx,
                                               host.cos.ctypes.data_as(fwgpu.fp), host.sin.ctypes.data_as(fwgpu.fp))
         assert rc == -1 and not h.value
-        assert "llama/qwen2 block" in fwgpu.last_error()
+        assert "llama/qwen2/gemma block" in fwgpu.last_error()
 
 
 def test_operator_argument_checks_match_reference():
@@ -117,7 +117,7 @@ def test_qwen2_synth_config():
     """A qwen2 file gets the architecture's block settings (model_config.c:161-168):
     q/k/v biases on, RoPE base raised to 1e6; the writer emits one F32 bias per
     q/k/v projection."""
-    sp = fwgpu.spec(256, 512, 2, 8, 2, 1000, 64, 10000.0, qkv_bias=True)
+    sp = fwgpu.spec(256, 512, 2, 8, 2, 1000, 64, 10000.0, arch="qwen2")
     with fwgpu.HostModel(synth=sp) as host:
         c = host.cfg
         assert c.arch == 3 and c.use_qkv_bias == 1 and c.rope_freq_base == 1e6

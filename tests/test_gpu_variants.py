@@ -1,12 +1,19 @@
-"""The qwen2 block on the GPU: llama's block plus F32 biases on the q, k and v
-projections (attention.c:114-126 via linear.c:214-221), added before RoPE, and
-the RoPE base the config loader raises to 1e6 (model_config.c:161-168).
+"""Architecture variants of the RMSNorm / gated-FFN block on the GPU, each held
+to the oracle (whose forward for each is pinned bit-exactly to the reference by
+a golden model fixture) on every decode path: the persistent step kernel, the
+per-phase kernels and the batched prefill.
 
-Every decode path adds the bias in its own epilogue: the persistent step
-kernel, the per-phase kernels (fused QKV launch, and separate launches when
-q/k/v types differ) and the batched prefill.  Each is held to the oracle, whose
-qwen2 forward is pinned bit-exactly to the reference by the "qwen2" golden
-fixture.  Bar: logits and the residual stream within max-abs 2e-3 / rel 1e-3,
+qwen2: llama's block plus F32 biases on the q, k and v projections
+(attention.c:114-126 via linear.c:214-221), added before RoPE, and the RoPE
+base the config loader raises to 1e6 (model_config.c:161-168).
+
+gemma: the gated FFN with the tanh GELU (ffn.c:33-42, model_config.c:170-176),
+embedding rows times sqrt(n_embd) (transformer.c:179-182) and, with no
+output.weight in the file, the lm-head read from token_embd
+(transformer.c:309-316).  The erf GELU (ffn.c:27-31) is run through the same
+kernels by selecting it in the config.
+
+Bar: logits and the residual stream within max-abs 2e-3 / rel 1e-3,
 identical greedy tokens."""
 import os
 
@@ -45,7 +52,7 @@ class env:
 
 def qwen2_q4(seed=21):
     # head_dim 64, GQA group 4, Q4_0 layers (the persistent kernel's shape class)
-    return fwgpu.spec(512, 1536, 2, 8, 2, 2048, 96, 10000.0, linear_type=Q4, seed=seed, qkv_bias=True)
+    return fwgpu.spec(512, 1536, 2, 8, 2, 2048, 96, 10000.0, linear_type=Q4, seed=seed, arch="qwen2")
 
 
 @pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_phase"])
@@ -107,3 +114,58 @@ def test_qwen2_prefill_matches_oracle():
                 kr, vr = om.kv(layer, pos)
                 close(k[pos], kr, f"K row layer {layer} pos {pos}")
                 close(v[pos], vr, f"V row layer {layer} pos {pos}")
+
+
+def gemma_q4(seed=31):
+    return fwgpu.spec(512, 1536, 2, 8, 2, 2048, 96, 10000.0, linear_type=Q4, seed=seed, arch="gemma")
+
+
+@pytest.mark.parametrize("act", ["gelu_tanh", "gelu_erf"])
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_phase"])
+def test_gemma_decode_matches_oracle(persistent, act):
+    fw_cpu.set_threads(8)
+    with env(**({} if persistent else {"FORWORD_GPU_MEGAKERNEL": "0"})):
+        with fwgpu.HostModel(synth=gemma_q4()) as host:
+            assert host.cfg.act_type == 2 and host.cfg.embd_scale == np.float32(np.sqrt(512))
+            if act == "gelu_erf":
+                host.cfg.act_type = 1
+            with fwgpu.GpuModel(host) as gm, fw_cpu.OracleModel(host) as om:
+                assert gm.persistent == persistent
+                toks = np.random.default_rng(8).integers(3, host.cfg.n_vocab, 10)
+                for pos, t in enumerate(toks):
+                    lg, ref = gm.forward(int(t), pos), om.forward(int(t), pos)
+                    close(lg, ref, f"{act} logits at position {pos}")
+                    assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+                    if pos in (0, 9):
+                        close(gm.layer_trace().reshape(-1), om.trace().reshape(-1), f"residual stream at {pos}")
+                got = gm.generate_greedy(toks[:4].astype(np.uint32), 12)
+                om_toks = om.generate_greedy(toks[:4].astype(np.uint32), 12)
+                assert np.array_equal(got, om_toks)
+
+
+def test_gemma_fixture_per_phase_matches_reference():
+    prompt = gs.prompt("gemma")
+    gold = gold_model("gemma")
+    m = gs.MODELS["gemma"]
+    with env(FORWORD_GPU_MEGAKERNEL="0"):
+        with fwgpu.HostModel(synth=m["spec"](), max_ctx=m["max_ctx"]) as host, fwgpu.GpuModel(host) as gm:
+            toks = gold["tokens"]
+            for f in range(gs.n_forwards("gemma")):
+                lg = gm.forward(int(toks[f]), f)
+                assert fw_cpu.argmax(lg) == int(gold["stats"][f, 0]), f"greedy choice differs at forward {f}"
+                if f in gs.logit_steps("gemma"):
+                    close(lg, gold[f"logits_{f}"], f"logits at forward {f}")
+            got = gm.generate_greedy(prompt, m["n_gen"])
+    assert np.array_equal(got, gold["tokens"][len(prompt):])
+
+
+def test_gemma_prefill_matches_oracle():
+    fw_cpu.set_threads(8)
+    with fwgpu.HostModel(synth=gemma_q4(seed=32)) as host, fwgpu.GpuModel(host) as gm, \
+            fw_cpu.OracleModel(host) as om:
+        prompt = np.random.default_rng(9).integers(3, host.cfg.n_vocab, 40).astype(np.uint32)
+        lg = gm.prefill(prompt)
+        for pos, t in enumerate(prompt):
+            ref = om.forward(int(t), pos)
+        close(lg, ref, "prefill logits")
+        assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)

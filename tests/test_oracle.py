@@ -269,6 +269,24 @@ def test_silu_matches_reference(gold_ops):
     assert np.array_equal(bits(fw_cpu.silu(gs.silu_input())), bits(gold_ops["silu"]))
 
 
+def test_gelu_forms_match_closed_form():
+    """apply_gelu (ffn.c:27-31) and apply_gelu_fast (ffn.c:33-42) against their
+    formulas in float64: 0.5 v (1 + erf(v/sqrt 2)) and 0.5 v (1 + tanh(sqrt(2/pi)
+    (v + 0.044715 v^3))).  The tanh form is also pinned bit-exactly by the gemma
+    model fixture; the erf form (no gated architecture selects it) only here.
+    A swapped constant, a dropped 0.5 or the other form fails by far more than
+    the float rounding allowed."""
+    import math
+    x = np.concatenate([np.linspace(-8, 8, 4001, dtype=np.float32), gs.silu_input()]).astype(np.float32)
+    xd = x.astype(np.float64)
+    erf_ref = 0.5 * xd * (1.0 + np.array([math.erf(v / math.sqrt(2.0)) for v in xd]))
+    tanh_ref = 0.5 * xd * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd ** 3)))
+    for got, ref in ((fw_cpu.gelu(x), erf_ref), (fw_cpu.gelu_fast(x), tanh_ref)):
+        err = np.abs(got.astype(np.float64) - ref)
+        assert np.all(err <= 4e-7 * np.maximum(np.abs(ref), 1.0)), float(err.max())
+    assert np.max(np.abs(erf_ref - tanh_ref)) > 1e-4          # the two forms are distinguishable
+
+
 def test_dot_matches_reference(gold_ops):
     got = np.array([fw_cpu.dot(*gs.dot_inputs(n)) for n in gs.DOT_SIZES], np.float32)
     assert np.array_equal(bits(got), bits(gold_ops["dot"]))
