@@ -363,7 +363,10 @@ __device__ __forceinline__ float gelu_tanh(float v)
 
 __device__ __forceinline__ float ffn_act(float v, uint32_t act)
 {
-    return act == ACT_GELU ? gelu_erf(v) : act == ACT_GELU_TANH ? gelu_tanh(v) : silu_ref(v);
+    return act == ACT_GELU        ? gelu_erf(v)
+         : act == ACT_GELU_TANH ? gelu_tanh(v)
+         : act == ACT_RELU      ? (v < 0.0f ? 0.0f : v)
+                                : silu_ref(v);
 }
 
 } // namespace fw

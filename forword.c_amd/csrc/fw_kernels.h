@@ -25,7 +25,7 @@ enum Epi : int { EPI_STORE = 0, EPI_QKV = 1, EPI_RESID = 2, EPI_SWIGLU = 3 };
 
 // Activation codes of the gated FFN (ffn.c:88-101): silu (also the default for
 // any other code), gelu with erf (ffn.c:27-31), gelu with tanh (ffn.c:33-42).
-enum FfnAct : uint32_t { ACT_SILU = 0, ACT_GELU = 1, ACT_GELU_TANH = 2 };
+enum FfnAct : uint32_t { ACT_SILU = 0, ACT_GELU = 1, ACT_GELU_TANH = 2, ACT_RELU = 3 };
 
 // One GEMV launch over up to three weight matrices that share the input x and
 // the column count (fused QKV; gate+up).  Rows of matrix s are rows[s].
@@ -43,7 +43,10 @@ struct QmvArgs {
                                // RESID: residual stream x (updated in place); SWIGLU: h
     float *trace;              // RESID: copy of the updated residual (may be null)
     const float *cos_tab, *sin_tab;
-    const float *bias[3];      // QKV: F32 bias by role (attn_{q,k,v}.bias) added before RoPE, or null
+    const float *bias[3];      // QKV: F32 bias by role (attn_{q,k,v}.bias) added before RoPE;
+                               // STORE: by segment; RESID: bias[0] added to the product; or null
+    const float *addend;       // RESID: x += addend + product (parallel residual), or null
+    float *trace2;             // RESID: second copy of the updated residual (may be null)
     const StepState *state;
     uint32_t head_dim;
     uint32_t kv_dim;           // n_head_kv * head_dim (K/V cache row length)
@@ -99,6 +102,15 @@ uint32_t argmax_blocks(uint32_t n);
 hipError_t launch_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t head_dim, const float *cos_tab,
                        const float *sin_tab, int neox, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s);
+// out = act(x) in place or not, FfnAct code (ffn.c:143-160, plain FFN).
+hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s);
+// layer_norm (norm.c:18-40) of one row of n floats; w and b may be null.
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, uint32_t n, float eps,
+                            hipStream_t s);
+// NEOX RoPE (rope.c:44-51) at the step's position: q heads in place and the K
+// cache row at pos of this layer.
+hipError_t launch_rope_neox_step(float *q, float *kc_layer, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                                 const float *cos_tab, const float *sin_tab, const StepState *st, hipStream_t s);
 // out = act(g) * u with an FfnAct code (ffn.c:88-104).
 hipError_t launch_act_mul(const float *g, const float *u, float *out, uint64_t n, uint32_t act, hipStream_t s);
 hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s);

@@ -248,16 +248,20 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
         if (lane == 0)
 #pragma unroll
             for (int k = 0; k < R; k++)
-                if (ok[k]) a.out[seg][row[k]] = acc[k];
+                if (ok[k]) a.out[seg][row[k]] = a.bias[seg] ? acc[k] + a.bias[seg][row[k]] : acc[k];
     } else if constexpr (EPI == EPI_RESID) {
         float ss = 0.f;
         if (lane == 0)
 #pragma unroll
             for (int k = 0; k < R; k++)
                 if (ok[k]) {
-                    float v = a.out[0][row[k]] + acc[k];          // x[i] += y[i] (transformer.c:271-272)
+                    float y = acc[k];
+                    if (a.bias[0]) y += a.bias[0][row[k]];          // linear.c:214-221
+                    if (a.addend) y = a.addend[row[k]] + y;         // attn_out + ffn_out (transformer.c:250-251)
+                    float v = a.out[0][row[k]] + y;                 // x[i] += y[i] (transformer.c:271-272)
                     a.out[0][row[k]] = v;
                     if (a.trace) a.trace[row[k]] = v;
+                    if (a.trace2) a.trace2[row[k]] = v;
                     ss = __builtin_fmaf(v, v, ss);
                 }
         if (a.scale_out) publish_norm_scale(ss, a.pss, a.ticket, a.scale_out, a.rows[0], a.norm_eps);
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
             float v[R];
 #pragma unroll
             for (int k = 0; k < R; k++) v[k] = bias && ok[k] ? acc[k] + bias[row[k]] : acc[k];
-            if (role < 2) {
+            if (role < 2 && a.cos_tab) {                         // no cos_tab: RoPE runs after (NEOX)
 #pragma unroll
                 for (int k = 0; k < R; k += 2) {
                     uint32_t i = (row[k] % a.head_dim) / 2;
@@ -817,6 +821,88 @@ static uint32_t ew_blocks(uint64_t n)
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s)
 {
     hipLaunchKernelGGL(k_silu_mul, dim3(ew_blocks(n)), dim3(256), 0, s, g, u, out, n);
+    return hipGetLastError();
+}
+
+__global__ void k_act(const float *x, float *out, uint64_t n, uint32_t act)
+{
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = ffn_act(x[i], act);
+}
+
+hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_act, dim3(ew_blocks(n)), dim3(256), 0, s, x, out, n, act);
+    return hipGetLastError();
+}
+
+__device__ __forceinline__ double block_sum_d(double v, double *s)
+{
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    __syncthreads();
+    if (lane == 0) s[w] = v;
+    __syncthreads();
+    double r = 0.0;
+    for (uint32_t i = 0; i < blockDim.x / 64; i++) r += s[i];
+    return r;
+}
+
+// layer_norm (norm.c:18-40): one workgroup; mean and variance summed in double
+// (the reference sums them in index order, here in a tree: the same doubles up
+// to the last bits, the same floats after rounding but for ties).
+__global__ __launch_bounds__(1024) void k_layernorm(const float *__restrict__ x, const float *__restrict__ w,
+                                                    const float *__restrict__ b, float *__restrict__ out,
+                                                    uint32_t n, float eps)
+{
+    __shared__ double s[16];
+    const uint32_t t = threadIdx.x;
+    double acc = 0.0;
+    for (uint32_t i = t; i < n; i += blockDim.x) acc += x[i];
+    const float mean = (float)(block_sum_d(acc, s) / (double)n);
+    double var = 0.0;
+    for (uint32_t i = t; i < n; i += blockDim.x) {
+        const float d = x[i] - mean;
+        var += (double)d * d;
+    }
+    const float scale = 1.0f / sqrtf((float)(block_sum_d(var, s) / (double)n) + eps);
+    for (uint32_t i = t; i < n; i += blockDim.x) {
+        float v = (x[i] - mean) * scale;
+        if (w) v *= w[i];
+        if (b) v += b[i];
+        out[i] = v;
+    }
+}
+
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, uint32_t n, float eps,
+                            hipStream_t s)
+{
+    hipLaunchKernelGGL(k_layernorm, dim3(1), dim3(1024), 0, s, x, w, b, out, n, eps);
+    return hipGetLastError();
+}
+
+// Pairs (v[i], v[half + i]) of every q head and of the K cache row at the
+// step's position (rope.c:44-51).
+__global__ void k_rope_neox_step(float *q, float *kc, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                                 const float *cos_tab, const float *sin_tab, const StepState *st)
+{
+    const uint32_t half = hd / 2, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (n_head + n_kv) * half) return;
+    const uint32_t head = i / half, p = i % half, pos = st->pos;
+    float *v = head < n_head ? q + (size_t)head * hd : kc + ((size_t)pos * n_kv + (head - n_head)) * hd;
+    const float c = cos_tab[(size_t)pos * half + p], s = sin_tab[(size_t)pos * half + p];
+    const float v0 = v[p], v1 = v[half + p];
+    v[p] = v0 * c - v1 * s;
+    v[half + p] = v0 * s + v1 * c;
+}
+
+hipError_t launch_rope_neox_step(float *q, float *kc_layer, uint32_t n_head, uint32_t n_kv, uint32_t hd,
+                                 const float *cos_tab, const float *sin_tab, const StepState *st, hipStream_t s)
+{
+    const uint32_t n = (n_head + n_kv) * (hd / 2);
+    hipLaunchKernelGGL(k_rope_neox_step, dim3((n + 255) / 256), dim3(256), 0, s, q, kc_layer, n_head, n_kv, hd,
+                       cos_tab, sin_tab, st);
     return hipGetLastError();
 }
 

@@ -61,6 +61,8 @@ struct Lin {
 
 struct Layer {
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    const float *attn_norm_b = nullptr, *ffn_norm_b = nullptr;   // LayerNorm biases, or null
+    const float *bo = nullptr;     // attn_output.bias, or null
     const float *bqkv = nullptr;   // attn_q|k|v.bias concatenated [n_embd + 2 kv_dim] (qwen2), or null
     Lin q, k, v, o, gate, up, down;
 };
@@ -85,6 +87,16 @@ static uint32_t ffn_act_code(const forword_gpu_config_t &c)
     return c.act_type == FORWORD_ACT_GELU        ? fw::ACT_GELU
          : c.act_type == FORWORD_ACT_GELU_FAST ? fw::ACT_GELU_TANH
                                                : fw::ACT_SILU;
+}
+
+// The plain FFN's activation (ffn.c:143-160): GELU-tanh, silu, relu by their
+// codes, GELU (erf) for GELU and every other code.
+static uint32_t plain_act_code(const forword_gpu_config_t &c)
+{
+    return c.act_type == FORWORD_ACT_GELU_FAST ? fw::ACT_GELU_TANH
+         : c.act_type == FORWORD_ACT_SILU      ? fw::ACT_SILU
+         : c.act_type == FORWORD_ACT_RELU      ? fw::ACT_RELU
+                                               : fw::ACT_GELU;
 }
 
 // Values per block of a block type (gguf.c:211-223); 1 for F32, 0 unknown.
@@ -115,6 +127,12 @@ struct forword_gpu {
     uint32_t *d_pi = nullptr, *d_counter = nullptr, *d_argmax = nullptr, *d_prompt = nullptr, *d_ids = nullptr;
     float *d_pss = nullptr, *d_scale = nullptr;      // RMSNorm scale published by the residual kernels
     float *d_bias = nullptr;                         // per-layer q|k|v biases (qwen2)
+    const float *out_norm_b = nullptr;               // output_norm.bias (LayerNorm), or null
+    // Blocks other than the RMSNorm / gated-FFN / sequential / pairwise-RoPE one
+    // (LayerNorm, parallel residual, plain FFN, NEOX RoPE, output-projection
+    // bias) run the explicit per-phase step (enqueue_step_generic).
+    bool generic = false;
+    float *d_ao = nullptr;                           // attention output kept for the parallel residual
     uint32_t *d_ticket = nullptr;
     StepState *d_state = nullptr, *h_state = nullptr;
     float *h_logits = nullptr;
@@ -215,8 +233,114 @@ static int bind_vec(forword_gpu_t *h, const float **p, const forword_gpu_tensor_
 
 // ── one token step ───────────────────────────────────────────────────────────
 
+// The block's pre-norm written out (transformer.c:234-239, 256-261, 275-280).
+static hipError_t launch_block_norm(const forword_gpu_t *h, const float *x, const float *w, const float *b, float *out,
+                                    hipStream_t s)
+{
+    const forword_gpu_config_t &c = h->cfg;
+    if (c.norm_type == FORWORD_NORM_LAYER) return launch_layernorm(x, w, b, out, c.n_embd, c.norm_eps, s);
+    return launch_rmsnorm(x, w, out, c.n_embd, c.norm_eps, s);
+}
+
+// One token step of any supported block (transformer.c:149-326): LayerNorm or
+// RMSNorm written out to xn, sequential or parallel residual, gated or plain
+// FFN, pairwise or NEOX RoPE, biases of q/k/v and of the output projection.
+static hipError_t enqueue_step_generic(forword_gpu_t *h)
+{
+    const forword_gpu_config_t &c = h->cfg;
+    const uint32_t n = c.n_embd, hd = c.head_dim, kvd = c.n_head_kv * hd;
+    const bool neox = c.rope_type == FORWORD_ROPE_NEOX, par = c.parallel_res != 0;
+    hipStream_t s = h->stream;
+    hipError_t e;
+#define TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
+    TRY(launch_embed(h->embd.w, h->embd.type, n, h->embd.out, h->d_state, nullptr, c.embd_scale, h->d_x,
+                     h->d_scale, c.norm_eps, s));                                       // transformer.c:167-182
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const Layer &Ly = h->L[l];
+        float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
+        TRY(launch_block_norm(h, h->d_x, Ly.attn_norm, Ly.attn_norm_b, h->d_xn, s));
+        const Lin *qkv[3] = { &Ly.q, &Ly.k, &Ly.v };                                   // attention.c:97-140
+        const bool fused = Ly.q.type == Ly.k.type && Ly.k.type == Ly.v.type;
+        for (uint32_t s0 = 0; s0 < 3; s0 += fused ? 3 : 1) {
+            QmvArgs a{};
+            a.n_seg = fused ? 3 : 1;
+            for (uint32_t i = 0; i < a.n_seg; i++) { a.w[i] = qkv[s0 + i]->w; a.rows[i] = qkv[s0 + i]->out; }
+            a.role_base = s0;
+            a.n_cols = n;
+            a.row_bytes = qkv[s0]->row_bytes;
+            a.x = h->d_xn;
+            a.out[0] = h->d_q; a.out[1] = kc; a.out[2] = vc;
+            if (!neox) { a.cos_tab = h->d_cos; a.sin_tab = h->d_sin; }
+            if (Ly.bqkv) { a.bias[0] = Ly.bqkv; a.bias[1] = Ly.bqkv + n; a.bias[2] = Ly.bqkv + n + kvd; }
+            a.state = h->d_state;
+            a.head_dim = hd;
+            a.kv_dim = kvd;
+            qmv_plan(a, EPI_QKV);
+            TRY(launch_qmv(qkv[s0]->type, EPI_QKV, a, s));
+        }
+        if (neox) TRY(launch_rope_neox_step(h->d_q, kc, c.n_head, c.n_head_kv, hd, h->d_cos, h->d_sin, h->d_state, s));
+        TRY(launch_attention(h->d_q, kc, vc, h->d_part, h->d_att, c.n_head, c.n_head_kv, hd, h->n_splits,
+                             h->d_state, 0, s));                                        // attention.c:142-164
+        {
+            QmvArgs a{};                                                                // attention.c:166
+            a.n_seg = 1; a.w[0] = Ly.o.w; a.rows[0] = Ly.o.out; a.n_cols = Ly.o.in; a.row_bytes = Ly.o.row_bytes;
+            a.x = h->d_att; a.bias[0] = Ly.bo;
+            if (par) {                                                                  // kept for the parallel add
+                a.out[0] = h->d_ao;
+                qmv_plan(a, EPI_STORE);
+                TRY(launch_qmv(Ly.o.type, EPI_STORE, a, s));
+            } else {                                                                    // transformer.c:271-272
+                a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l) * n;
+                qmv_plan(a, EPI_RESID);
+                TRY(launch_qmv(Ly.o.type, EPI_RESID, a, s));
+                TRY(launch_block_norm(h, h->d_x, Ly.ffn_norm, Ly.ffn_norm_b, h->d_xn, s));   // transformer.c:275-280
+            }
+        }
+        if (c.use_ffn_gate) {                                                           // ffn.c:68-104
+            QmvArgs a{};
+            a.n_seg = 2; a.w[0] = Ly.gate.w; a.w[1] = Ly.up.w; a.rows[0] = a.rows[1] = c.n_ff;
+            a.n_cols = n; a.row_bytes = Ly.gate.row_bytes; a.x = h->d_xn; a.out[0] = h->d_h;
+            a.act = ffn_act_code(c);
+            qmv_plan(a, EPI_SWIGLU);
+            TRY(launch_qmv(Ly.gate.type, EPI_SWIGLU, a, s));
+        } else {                                                                        // ffn.c:108-160
+            QmvArgs a{};
+            a.n_seg = 1; a.w[0] = Ly.up.w; a.rows[0] = c.n_ff; a.n_cols = n; a.row_bytes = Ly.up.row_bytes;
+            a.x = h->d_xn; a.out[0] = h->d_h;
+            qmv_plan(a, EPI_STORE);
+            TRY(launch_qmv(Ly.up.type, EPI_STORE, a, s));
+            TRY(launch_act(h->d_h, h->d_h, c.n_ff, plain_act_code(c), s));
+        }
+        {
+            QmvArgs a{};                                                                // ffn.c:106/168, transformer.c:250/287
+            a.n_seg = 1; a.w[0] = Ly.down.w; a.rows[0] = n; a.n_cols = c.n_ff; a.row_bytes = Ly.down.row_bytes;
+            a.x = h->d_h; a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l + 1) * n;
+            if (par) { a.addend = h->d_ao; a.trace2 = h->d_trace + (size_t)(2 * l) * n; }
+            qmv_plan(a, EPI_RESID);
+            TRY(launch_qmv(Ly.down.type, EPI_RESID, a, s));
+        }
+    }
+    const float *xh = h->d_x;                                                          // transformer.c:293-307
+    if (h->out_norm) {
+        TRY(launch_block_norm(h, h->d_x, h->out_norm, h->out_norm_b, h->d_xn, s));
+        xh = h->d_xn;
+    }
+    {
+        QmvArgs a{};                                                                    // transformer.c:309-323
+        a.n_seg = 1; a.w[0] = h->out.w; a.rows[0] = h->out.out; a.n_cols = n; a.row_bytes = h->out.row_bytes;
+        a.x = xh; a.out[0] = h->d_logits; a.state = h->d_state;
+        qmv_plan(a, EPI_STORE);
+        TRY(launch_qmv(h->out.type, EPI_STORE, a, s));
+    }
+    TRY(launch_argmax(h->d_logits, c.n_vocab, h->d_pv, h->d_pi, h->d_counter, h->d_argmax, h->d_state, h->d_prompt,
+                      h->d_ids, h->am_blocks, s));
+#undef TRY
+    return hipSuccess;
+}
+
 static hipError_t enqueue_step(forword_gpu_t *h)
 {
+    if (h->generic) return enqueue_step_generic(h);
     const forword_gpu_config_t &c = h->cfg;
     const uint32_t n = c.n_embd, hd = c.head_dim, kvd = c.n_head_kv * hd;
     hipStream_t s = h->stream;
@@ -344,7 +468,7 @@ static int mk_check(forword_gpu_t *h)
 static int setup_mk(forword_gpu_t *h)
 {
     const char *env = getenv("FORWORD_GPU_MEGAKERNEL");
-    if (env && !strcmp(env, "0")) return 0;
+    if ((env && !strcmp(env, "0")) || h->generic) return 0;
     const forword_gpu_config_t &c = h->cfg;
     const uint32_t n = c.n_embd, hd = c.head_dim, L = c.n_layer;
     const uint32_t tl = h->L[0].q.type;
@@ -490,9 +614,10 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         set_err("forword_gpu_init: invalid model dimensions");
         return -1;
     }
-    if (c.norm_type != FORWORD_NORM_RMS || !c.use_ffn_gate || c.parallel_res || c.rope_type != FORWORD_ROPE_NORMAL) {
-        set_err("forword_gpu_init: only the llama/qwen2/gemma block (RMSNorm, gated FFN, RoPE pairs (2i,2i+1), "
-                "sequential residual) is implemented");
+    if ((c.norm_type != FORWORD_NORM_RMS && c.norm_type != FORWORD_NORM_LAYER) || c.arch == FORWORD_ARCH_GPT2 ||
+        (c.rope_type != FORWORD_ROPE_NORMAL && c.rope_type != FORWORD_ROPE_NEOX)) {
+        set_err("forword_gpu_init: GPT-2 style blocks (fused QKV, learned positions, no RoPE) and unknown "
+                "norm/RoPE types are not implemented");
         return -1;
     }
     if (!attn_supported(c.head_dim, c.n_head / c.n_head_kv)) {
@@ -528,7 +653,8 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
     if (!to) to = te;                                                                   // transformer.c:310-316
     if (bind_lin(h, h->embd, te, "token_embd.weight", n, c.n_vocab)) FAIL();
     if (bind_lin(h, h->out, to, "output.weight", n, c.n_vocab)) FAIL();
-    if (bind_vec(h, &h->out_norm, find_t(tensors, n_tensors, "output_norm.weight"), "output_norm.weight", n, false))
+    if (bind_vec(h, &h->out_norm, find_t(tensors, n_tensors, "output_norm.weight"), "output_norm.weight", n, false) ||
+        bind_vec(h, &h->out_norm_b, find_t(tensors, n_tensors, "output_norm.bias"), "output_norm.bias", n, false))
         FAIL();
     h->L.resize(c.n_layer);
     for (uint32_t l = 0; l < c.n_layer; l++) {
@@ -541,18 +667,37 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         LIN(k, "attn_k.weight", n, kvd);
         LIN(v, "attn_v.weight", n, kvd);
         LIN(o, "attn_output.weight", n, n);
-        LIN(gate, "ffn_gate.weight", n, c.n_ff);
-        LIN(up, "ffn_up.weight", n, c.n_ff);
-        LIN(down, "ffn_down.weight", c.n_ff, n);
+        if (c.use_ffn_gate) {
+            LIN(gate, "ffn_gate.weight", n, c.n_ff);
+            LIN(up, "ffn_up.weight", n, c.n_ff);
+            LIN(down, "ffn_down.weight", c.n_ff, n);
+            if (Ly.gate.type != Ly.up.type) { set_err("layer %u: ffn_gate and ffn_up types differ", l); FAIL(); }
+        } else {                                    // plain FFN (ffn.c:110-168), fc1/fc2 names too
+            snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l);
+            const forword_gpu_tensor_t *tu = find_t(tensors, n_tensors, nm);
+            if (!tu) { snprintf(nm, sizeof nm, "blk.%u.fc1.weight", l); tu = find_t(tensors, n_tensors, nm); }
+            if (bind_lin(h, Ly.up, tu, nm, n, c.n_ff)) FAIL();
+            snprintf(nm, sizeof nm, "blk.%u.fc2.weight", l);
+            const forword_gpu_tensor_t *td = find_t(tensors, n_tensors, nm);
+            if (!td) { snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); td = find_t(tensors, n_tensors, nm); }
+            if (bind_lin(h, Ly.down, td, nm, c.n_ff, n)) FAIL();
+        }
 #undef LIN
-        if (Ly.gate.type != Ly.up.type) { set_err("layer %u: ffn_gate and ffn_up types differ", l); FAIL(); }
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l);
         if (bind_vec(h, &Ly.attn_norm, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
-        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);
-        if (bind_vec(h, &Ly.ffn_norm, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
+        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);                         // unused by a parallel block
+        if (bind_vec(h, &Ly.ffn_norm, find_t(tensors, n_tensors, nm), nm, n, !c.parallel_res)) FAIL();
+        snprintf(nm, sizeof nm, "blk.%u.attn_norm.bias", l);                          // transformer.c:212-230
+        if (bind_vec(h, &Ly.attn_norm_b, find_t(tensors, n_tensors, nm), nm, n, false)) FAIL();
+        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.bias", l);
+        if (bind_vec(h, &Ly.ffn_norm_b, find_t(tensors, n_tensors, nm), nm, n, false)) FAIL();
         snprintf(nm, sizeof nm, "blk.%u.attn_output.bias", l);                        // attention.c:106-107
-        if (find_t(tensors, n_tensors, nm)) { set_err("tensor %s: output-projection bias not implemented", nm); FAIL(); }
+        if (bind_vec(h, &Ly.bo, find_t(tensors, n_tensors, nm), nm, n, false)) FAIL();
+        if (Ly.bo) h->generic = true;
     }
+    if (c.norm_type != FORWORD_NORM_RMS || c.parallel_res || !c.use_ffn_gate || c.rope_type != FORWORD_ROPE_NORMAL)
+        h->generic = true;
+    if (c.parallel_res && dalloc(h, (void **)&h->d_ao, (size_t)n * 4, "attention output")) FAIL();
     if (c.use_qkv_bias) {
         // attention.c:114-122: the q/k/v biases of each layer, gathered into one
         // [n_embd | kv_dim | kv_dim] vector in the order the fused QKV rows use;
@@ -753,6 +898,16 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
     }
     for (size_t i = 0; i < n_tok; i++)
         if (tokens[i] >= c.n_vocab) { set_err("prefill: token %u out of range", tokens[i]); return -1; }
+    if (h->generic) {
+        // other blocks prefill token by token, as main.c:145-151 does; each step's
+        // state upload reads the pinned staging copy, so the host waits for the
+        // step before rewriting it
+        for (size_t i = 0; i < n_tok; i++) {
+            if (step_once(h, tokens[i], pos0 + i)) return -1;
+            HIPCHK(hipStreamSynchronize(h->stream), "prefill step");
+        }
+        return 0;
+    }
     const uint32_t n = c.n_embd, hd = c.head_dim, nq = c.n_head * hd, kvd = c.n_head_kv * hd, nff = c.n_ff;
     for (const Layer &Ly : h->L)
         for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })

@@ -31,7 +31,7 @@ GGML_F32, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 2, 6, 8, 12
 BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q5_0: 22, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
 BLOCK_VALUES = {GGML_Q4_0: 32, GGML_Q5_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
 # Architectures the synthetic writer emits, as FORWORD_ARCH_* values (model_config.h:12-24).
-SYNTH_ARCHS = {"llama": 2, "qwen2": 3, "gemma": 5}
+SYNTH_ARCHS = {"llama": 2, "qwen2": 3, "gemma": 5, "phi2": 6}
 TYPE_NAMES = {GGML_F32: "F32", GGML_Q4_0: "Q4_0", GGML_Q5_0: "Q5_0", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K",
               GGML_Q6_K: "Q6_K"}
 
@@ -68,7 +68,9 @@ def spec(n_embd, n_ff, n_layer, n_head, n_head_kv, n_vocab, n_ctx, rope_freq_bas
          norm_eps=1e-5, linear_type=GGML_Q8_0, embd_type=GGML_Q8_0, output_type=GGML_Q8_0,
          seed=1, w_std=0.02, norm_std=0.01, threads=0, arch="llama") -> SynthSpec:
     """Synthetic model shape.  arch "qwen2" adds attn_{q,k,v}.bias per layer; "gemma"
-    (gated GELU-tanh FFN, embedding times sqrt(n_embd)) ties the lm-head to token_embd."""
+    (gated GELU-tanh FFN, embedding times sqrt(n_embd)) ties the lm-head to token_embd;
+    "phi2" is the LayerNorm / parallel-residual / plain-FFN / NEOX-RoPE block with norm
+    and output-projection biases."""
     return SynthSpec(n_embd, n_ff, n_layer, n_head, n_head_kv, n_vocab, n_ctx, rope_freq_base,
                      norm_eps, linear_type, embd_type, output_type, seed, w_std, norm_std, threads,
                      SYNTH_ARCHS[arch])

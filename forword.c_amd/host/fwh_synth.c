@@ -384,7 +384,8 @@ static int token_text(uint32_t i, char *buf) { return sprintf(buf, "<t%u>", i); 
 /* Architectures the writer emits (model_config.c:10-22 names). */
 static const char *synth_arch_name(uint32_t arch)
 {
-    return arch == FORWORD_ARCH_QWEN2 ? "qwen2" : arch == FORWORD_ARCH_GEMMA ? "gemma" : "llama";
+    return arch == FORWORD_ARCH_QWEN2 ? "qwen2" : arch == FORWORD_ARCH_GEMMA ? "gemma"
+         : arch == FORWORD_ARCH_PHI2 ? "phi2" : "llama";
 }
 
 static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
@@ -399,12 +400,14 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         s->n_embd % fwh_block_values(s->output_type))
         return -1;
     uint64_t hd = s->n_embd / s->n_head, kvd = hd * s->n_head_kv;
-    L->t = (tdesc_t *)calloc(12 * (size_t)s->n_layer + 3, sizeof(tdesc_t));
+    const int phi2 = s->arch == FORWORD_ARCH_PHI2;
+    L->t = (tdesc_t *)calloc(12 * (size_t)s->n_layer + 6, sizeof(tdesc_t));
     if (!L->t) return -1;
     char nm[64];
     add_t(L, "token_embd.weight", T_EMBD, s->embd_type, s->n_embd, s->n_vocab, 2);
     for (uint32_t l = 0; l < s->n_layer; l++) {
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l); add_t(L, nm, T_ATTN_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
+        if (phi2) { snprintf(nm, sizeof nm, "blk.%u.attn_norm.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1); }
         snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, s->n_embd, 2);
         snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); add_t(L, nm, T_K, s->linear_type, s->n_embd, kvd, 2);
         snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, s->linear_type, s->n_embd, kvd, 2);
@@ -414,12 +417,15 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
             snprintf(nm, sizeof nm, "blk.%u.attn_v.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
         }
         snprintf(nm, sizeof nm, "blk.%u.attn_output.weight", l); add_t(L, nm, T_O, s->linear_type, s->n_embd, s->n_embd, 2);
+        if (phi2) { snprintf(nm, sizeof nm, "blk.%u.attn_output.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1); }
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l); add_t(L, nm, T_FFN_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
-        snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); add_t(L, nm, T_GATE, s->linear_type, s->n_embd, s->n_ff, 2);
+        if (phi2) { snprintf(nm, sizeof nm, "blk.%u.ffn_norm.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1); }
+        if (!phi2) { snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); add_t(L, nm, T_GATE, s->linear_type, s->n_embd, s->n_ff, 2); }
         snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l); add_t(L, nm, T_UP, s->linear_type, s->n_embd, s->n_ff, 2);
         snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); add_t(L, nm, T_DOWN, s->linear_type, s->n_ff, s->n_embd, 2);
     }
     add_t(L, "output_norm.weight", T_OUT_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
+    if (phi2) add_t(L, "output_norm.bias", T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1);
     if (s->arch != FORWORD_ARCH_GEMMA)
         add_t(L, "output.weight", T_OUT, s->output_type, s->n_embd, s->n_vocab, 2);
 

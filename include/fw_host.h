@@ -98,7 +98,9 @@ typedef struct {
     uint32_t threads;             /* 0 = default */
     uint32_t arch;                /* FORWORD_ARCH_*: 0 or LLAMA = llama; QWEN2 adds F32
                                      blk.N.attn_{q,k,v}.bias ~ N(0, 4*w_std); GEMMA writes
-                                     no output.weight (the head reuses token_embd) */
+                                     no output.weight (the head reuses token_embd); PHI2
+                                     writes no ffn_gate and adds F32 biases to the norms
+                                     (attn, ffn, output) and to attn_output */
 } fwh_synth_spec_t;
 
 /* Exact byte size of the GGUF image fwh_synth_write would produce. */

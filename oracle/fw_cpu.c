@@ -373,6 +373,27 @@ void fwc_silu(float *x, size_t n)
     }
 }
 
+/* layer_norm (norm.c:18-40): mean and variance summed in double in index
+ * order, then ((x - mean) * scale) * w + b per element, w and b optional. */
+void fwc_layer_norm(const float *x, const float *w, const float *b, float *out, size_t n, float eps)
+{
+    double sum = 0.0;
+    for (size_t i = 0; i < n; i++) sum += x[i];
+    const float mean = (float)(sum / (double)n);
+    double var = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        const float d = x[i] - mean;
+        var += (double)d * d;
+    }
+    const float scale = 1.0f / sqrtf((float)(var / (double)n) + eps);
+    for (size_t i = 0; i < n; i++) {
+        float v = (x[i] - mean) * scale;
+        if (w) v *= w[i];
+        if (b) v += b[i];
+        out[i] = v;
+    }
+}
+
 /* apply_gelu (ffn.c:27-31): 0.5 v (1 + erf(v / sqrt 2)), libm erff. */
 void fwc_gelu(float *x, size_t n)
 {
@@ -454,9 +475,9 @@ struct fwc_model {
     const uint8_t *data;
     size_t data_size;
     lin_t embd, out_w;
-    const float *out_norm;
+    const float *out_norm, *out_norm_b;
     struct layer {
-        const float *attn_norm, *ffn_norm;
+        const float *attn_norm, *ffn_norm, *attn_norm_b, *ffn_norm_b;
         const float *bq, *bk, *bv, *bo;    /* F32 biases, null when absent */
         lin_t q, k, v, o, gate, up, down;
     } *L;
@@ -505,8 +526,8 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
 {
     if (!data || !t || !cfg || !max_ctx || !cos_tab || !sin_tab) return NULL;
     const forword_gpu_config_t *c = cfg;
-    if (c->norm_type != FORWORD_NORM_RMS || !c->use_ffn_gate ||
-        c->parallel_res || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
+    if ((c->norm_type != FORWORD_NORM_RMS && c->norm_type != FORWORD_NORM_LAYER) ||
+        c->arch == FORWORD_ARCH_GPT2 || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
         c->n_head % c->n_head_kv || c->head_dim % 2 || c->n_embd != c->n_head * c->head_dim) {
         fprintf(stderr, "fwc_model_init: unsupported model variant\n");
         return NULL;
@@ -525,6 +546,7 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
     if (!o) o = e;
     if (bind_lin(&m->embd, m, e) || bind_lin(&m->out_w, m, o)) goto fail;
     m->out_norm = bind_vec(m, find(t, nt, "output_norm.weight"), c->n_embd);
+    m->out_norm_b = bind_vec(m, find(t, nt, "output_norm.bias"), c->n_embd);
     m->L = calloc(c->n_layer, sizeof(*m->L));
     if (!m->L) goto fail;
     for (uint32_t l = 0; l < c->n_layer; l++) {
@@ -533,9 +555,25 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
 #define LIN(field, suffix) snprintf(nm, sizeof nm, "blk.%u." suffix, l); \
         if (bind_lin(&L->field, m, find(t, nt, nm))) goto fail;
         LIN(q, "attn_q.weight"); LIN(k, "attn_k.weight"); LIN(v, "attn_v.weight");
-        LIN(o, "attn_output.weight"); LIN(gate, "ffn_gate.weight"); LIN(up, "ffn_up.weight");
-        LIN(down, "ffn_down.weight");
+        LIN(o, "attn_output.weight");
+        if (c->use_ffn_gate) {
+            LIN(gate, "ffn_gate.weight"); LIN(up, "ffn_up.weight"); LIN(down, "ffn_down.weight");
+        } else {                                     /* ffn.c:110-168: fc1 / fc2 names too */
+            snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l);
+            const forword_gpu_tensor_t *tu = find(t, nt, nm);
+            snprintf(nm, sizeof nm, "blk.%u.fc1.weight", l);
+            if (!tu) tu = find(t, nt, nm);
+            snprintf(nm, sizeof nm, "blk.%u.fc2.weight", l);
+            const forword_gpu_tensor_t *td = find(t, nt, nm);
+            snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l);
+            if (!td) td = find(t, nt, nm);
+            if (bind_lin(&L->up, m, tu) || bind_lin(&L->down, m, td)) goto fail;
+        }
 #undef LIN
+        snprintf(nm, sizeof nm, "blk.%u.attn_norm.bias", l);       /* transformer.c:212-230 */
+        L->attn_norm_b = bind_vec(m, find(t, nt, nm), c->n_embd);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.bias", l);
+        L->ffn_norm_b = bind_vec(m, find(t, nt, nm), c->n_embd);
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l);
         L->attn_norm = bind_vec(m, find(t, nt, nm), c->n_embd);
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l);
@@ -588,6 +626,36 @@ static void add_bias(float *y, const float *b, size_t n)
     if (b) for (size_t i = 0; i < n; i++) y[i] += b[i];
 }
 
+/* The block's pre-norm (transformer.c:234-239, 256-261, 275-280). */
+static void block_norm(const fwc_model_t *m, const float *w, const float *b)
+{
+    const forword_gpu_config_t *c = &m->c;
+    if (c->norm_type == FORWORD_NORM_LAYER) fwc_layer_norm(m->x, w, b, m->xn, c->n_embd, c->norm_eps);
+    else fwc_rms_norm(m->x, w, m->xn, c->n_embd, c->norm_eps);
+}
+
+/* ffn_forward (ffn.c:44-177) of m->xn into m->ffn_out: the gated branch
+ * (:68-107, silu by default) or the plain one (:108-171, gelu by default, relu). */
+static int ffn(fwc_model_t *m, const struct layer *L)
+{
+    const forword_gpu_config_t *c = &m->c;
+    const size_t nf = c->n_ff;
+    if (c->use_ffn_gate) {
+        if (lin(&L->gate, m->xn, m->gate) || lin(&L->up, m->xn, m->upb)) return -1;
+        if (c->act_type == FORWORD_ACT_GELU) fwc_gelu(m->gate, nf);
+        else if (c->act_type == FORWORD_ACT_GELU_FAST) fwc_gelu_fast(m->gate, nf);
+        else fwc_silu(m->gate, nf);
+        for (size_t i = 0; i < nf; i++) m->gate[i] *= m->upb[i];
+        return lin(&L->down, m->gate, m->ffn_out);
+    }
+    if (lin(&L->up, m->xn, m->upb)) return -1;
+    if (c->act_type == FORWORD_ACT_GELU_FAST) fwc_gelu_fast(m->upb, nf);
+    else if (c->act_type == FORWORD_ACT_SILU) fwc_silu(m->upb, nf);
+    else if (c->act_type == FORWORD_ACT_RELU) { for (size_t i = 0; i < nf; i++) if (m->upb[i] < 0.0f) m->upb[i] = 0.0f; }
+    else fwc_gelu(m->upb, nf);
+    return lin(&L->down, m->upb, m->ffn_out);
+}
+
 float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
 {
     const forword_gpu_config_t *c = &m->c;
@@ -596,10 +664,10 @@ float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
     if (get_row(&m->embd, token, m->x)) return NULL;             /* transformer.c:167-177 */
     if (c->embd_scale != 1.0f) for (size_t i = 0; i < n; i++) m->x[i] *= c->embd_scale;
     int neox = c->rope_type == FORWORD_ROPE_NEOX;
-    for (uint32_t l = 0; l < c->n_layer; l++) {                  /* transformer.c:255-289 */
+    for (uint32_t l = 0; l < c->n_layer; l++) {                  /* transformer.c:208-290 */
         struct layer *L = &m->L[l];
-        fwc_rms_norm(m->x, L->attn_norm, m->xn, n, c->norm_eps);
-        /* attention_forward (attention.c:124-166) */
+        block_norm(m, L->attn_norm, L->attn_norm_b);
+        /* attention_forward (attention.c:97-166) */
         if (lin(&L->q, m->xn, m->q) || lin(&L->k, m->xn, m->k) || lin(&L->v, m->xn, m->v)) return NULL;
         add_bias(m->q, L->bq, n);                                /* linear.c:214-221 */
         add_bias(m->k, L->bk, kvd);
@@ -612,21 +680,26 @@ float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
                            c->n_head_kv, hd, pos, m->scores);
         if (lin(&L->o, m->att, m->attn_out)) return NULL;
         add_bias(m->attn_out, L->bo, n);
+        if (c->parallel_res) {                                   /* transformer.c:232-252 */
+            if (ffn(m, L)) return NULL;
+            for (size_t i = 0; i < n; i++) m->x[i] += m->attn_out[i] + m->ffn_out[i];
+            memcpy(m->trace + (2 * (size_t)l) * n, m->x, n * 4);   /* one residual add: both rows */
+            memcpy(m->trace + (2 * (size_t)l + 1) * n, m->x, n * 4);
+            continue;
+        }
         for (size_t i = 0; i < n; i++) m->x[i] += m->attn_out[i];
         memcpy(m->trace + (2 * (size_t)l) * n, m->x, n * 4);
-        fwc_rms_norm(m->x, L->ffn_norm, m->xn, n, c->norm_eps);
-        /* ffn_forward gated branch (ffn.c:68-107) */
-        if (lin(&L->gate, m->xn, m->gate) || lin(&L->up, m->xn, m->upb)) return NULL;
-        if (c->act_type == FORWORD_ACT_GELU) fwc_gelu(m->gate, c->n_ff);       /* ffn.c:88-101 */
-        else if (c->act_type == FORWORD_ACT_GELU_FAST) fwc_gelu_fast(m->gate, c->n_ff);
-        else fwc_silu(m->gate, c->n_ff);                                        /* silu, also the default */
-        for (size_t i = 0; i < c->n_ff; i++) m->gate[i] *= m->upb[i];
-        if (lin(&L->down, m->gate, m->ffn_out)) return NULL;
+        block_norm(m, L->ffn_norm, L->ffn_norm_b);
+        if (ffn(m, L)) return NULL;
         for (size_t i = 0; i < n; i++) m->x[i] += m->ffn_out[i];
         memcpy(m->trace + (2 * (size_t)l + 1) * n, m->x, n * 4);
     }
-    if (m->out_norm) fwc_rms_norm(m->x, m->out_norm, m->xn, n, c->norm_eps);   /* transformer.c:293-307 */
-    else memcpy(m->xn, m->x, n * 4);
+    if (m->out_norm) {                                           /* transformer.c:293-307 */
+        if (c->norm_type == FORWORD_NORM_LAYER) fwc_layer_norm(m->x, m->out_norm, m->out_norm_b, m->xn, n, c->norm_eps);
+        else fwc_rms_norm(m->x, m->out_norm, m->xn, n, c->norm_eps);
+    } else {
+        memcpy(m->xn, m->x, n * 4);
+    }
     if (lin(&m->out_w, m->xn, m->logits)) return NULL;          /* transformer.c:310-323 */
     m->traced = 1;
     return m->logits;

@@ -48,6 +48,7 @@ void     fwc_softmax(float *x, size_t n);
 void     fwc_silu(float *x, size_t n);
 void     fwc_gelu(float *x, size_t n);
 void     fwc_gelu_fast(float *x, size_t n);
+void     fwc_layer_norm(const float *x, const float *w, const float *b, float *out, size_t n, float eps);
 uint32_t fwc_argmax(const float *x, size_t n);
 /* attention core (attention.c:142-164) over one layer's KV slice */
 void     fwc_attention_core(const float *q, const float *kc, const float *vc, float *out,

@@ -76,8 +76,24 @@ static int in_list(const char *list, size_t v)
     return 0;
 }
 
-/* transformer.c:149-326, RMSNorm / sequential-residual branch (llama, qwen2,
- * gemma), with the residual stream copied out after each residual add. */
+/* The block's pre-norm with the reference's own kernels (transformer.c:234-239). */
+static void pre_norm(const model_config_t *c, const float *x, const float *w, const float *b, float *out)
+{
+    if (c->norm_type == NORM_LAYER) layer_norm(x, w, b, out, c->n_embd, c->norm_eps);
+    else rms_norm(x, w, out, c->n_embd, c->norm_eps);
+}
+
+static const float *vec(const gguf_file_t *g, const char *fmt, size_t l)
+{
+    char nm[128];
+    snprintf(nm, sizeof nm, fmt, l);
+    const gguf_tensor_t *t = tensor_find(g, nm);
+    return t ? (const float *)tensor_data(g, t, NULL) : NULL;
+}
+
+/* transformer.c:149-326 (sequential and parallel residual, RMSNorm and
+ * LayerNorm), with the residual stream copied out after each residual add;
+ * a parallel-residual layer has one add, recorded in both of its rows. */
 static float *traced_forward(transformer_t *t, uint32_t tok, size_t pos, float *trace)
 {
     const model_config_t *c = &t->cfg;
@@ -87,23 +103,28 @@ static float *traced_forward(transformer_t *t, uint32_t tok, size_t pos, float *
     if (c->embd_scale != 1.0f)                                      /* transformer.c:179-182 */
         for (size_t i = 0; i < n; i++) t->x[i] *= c->embd_scale;
     for (size_t l = 0; l < c->n_layer; l++) {
-        char nm[128];
-        snprintf(nm, sizeof nm, "blk.%zu.attn_norm.weight", l);
-        const float *an = (const float *)tensor_data(g, tensor_find(g, nm), NULL);
-        snprintf(nm, sizeof nm, "blk.%zu.ffn_norm.weight", l);
-        const float *fn = (const float *)tensor_data(g, tensor_find(g, nm), NULL);
-        rms_norm(t->x, an, t->xn, n, c->norm_eps);
+        const float *an = vec(g, "blk.%zu.attn_norm.weight", l), *anb = vec(g, "blk.%zu.attn_norm.bias", l);
+        const float *fn = vec(g, "blk.%zu.ffn_norm.weight", l), *fnb = vec(g, "blk.%zu.ffn_norm.bias", l);
+        pre_norm(c, t->x, an, anb, t->xn);
         if (attention_forward(c, g, &t->kv, t->cos_tab, t->sin_tab, t->xn, t->attn_out, t->scratch, l, pos))
             return NULL;
+        if (c->parallel_res) {
+            if (ffn_forward(c, g, t->xn, t->ffn_out, t->scratch, l)) return NULL;
+            for (size_t i = 0; i < n; i++) t->x[i] += t->attn_out[i] + t->ffn_out[i];
+            memcpy(trace + 2 * l * n, t->x, n * 4);
+            memcpy(trace + (2 * l + 1) * n, t->x, n * 4);
+            continue;
+        }
         for (size_t i = 0; i < n; i++) t->x[i] += t->attn_out[i];
         memcpy(trace + 2 * l * n, t->x, n * 4);
-        rms_norm(t->x, fn, t->xn, n, c->norm_eps);
+        pre_norm(c, t->x, fn, fnb, t->xn);
         if (ffn_forward(c, g, t->xn, t->ffn_out, t->scratch, l)) return NULL;
         for (size_t i = 0; i < n; i++) t->x[i] += t->ffn_out[i];
         memcpy(trace + (2 * l + 1) * n, t->x, n * 4);
     }
-    const float *w = (const float *)tensor_data(g, tensor_find(g, "output_norm.weight"), NULL);
-    rms_norm(t->x, w, t->xn, n, c->norm_eps);
+    const float *w = vec(g, "output_norm.weight", 0), *b = vec(g, "output_norm.bias", 0);
+    if (w) pre_norm(c, t->x, w, b, t->xn);                          /* transformer.c:293-307 */
+    else memcpy(t->xn, t->x, n * 4);
     const gguf_tensor_t *ow = tensor_find(g, "output.weight");     /* transformer.c:309-316 */
     if (!ow) ow = tensor_find(g, "lm_head.weight");
     if (!ow) ow = tensor_find(g, "token_embd.weight");

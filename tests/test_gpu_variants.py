@@ -13,6 +13,15 @@ output.weight in the file, the lm-head read from token_embd
 (transformer.c:309-316).  The erf GELU (ffn.c:27-31) is run through the same
 kernels by selecting it in the config.
 
+phi2: LayerNorm with biases (norm.c:18-40), parallel residual
+(transformer.c:232-252), plain FFN with the tanh GELU (ffn.c:108-171), NEOX
+RoPE (rope.c:44-51) and the output-projection bias (attention.c:106-107), on
+the explicit per-phase step (the persistent kernel and the batched prefill
+serve the RMSNorm / gated / sequential / pairwise-RoPE block only; a phi2
+prefill runs token by token).  Config overrides on the same file run the
+remaining combinations: sequential LayerNorm, RMSNorm, pairwise RoPE, and the
+plain FFN's relu / silu / erf-GELU activations.
+
 Bar: logits and the residual stream within max-abs 2e-3 / rel 1e-3,
 identical greedy tokens."""
 import os
@@ -169,3 +178,69 @@ def test_gemma_prefill_matches_oracle():
             ref = om.forward(int(t), pos)
         close(lg, ref, "prefill logits")
         assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+
+
+PHI2_OVERRIDES = {
+    "phi2": {},
+    "sequential_layernorm": {"parallel_res": 0},
+    "rmsnorm": {"norm_type": 0},
+    "pairwise_rope": {"rope_type": 0},
+    "plain_relu": {"act_type": 3},
+    "plain_silu": {"act_type": 0},
+    "plain_gelu_erf": {"act_type": 1},
+}
+
+
+@pytest.mark.parametrize("variant", list(PHI2_OVERRIDES))
+def test_phi2_family_matches_oracle(variant):
+    fw_cpu.set_threads(8)
+    sp = fwgpu.spec(512, 1536, 2, 8, 8, 2048, 96, 10000.0, linear_type=Q4, seed=41, arch="phi2")
+    with fwgpu.HostModel(synth=sp) as host:
+        c = host.cfg
+        assert (c.norm_type, c.parallel_res, c.use_ffn_gate, c.rope_type, c.act_type) == (1, 1, 0, 1, 2)
+        for k, v in PHI2_OVERRIDES[variant].items():
+            setattr(host.cfg, k, v)
+        with fwgpu.GpuModel(host) as gm, fw_cpu.OracleModel(host) as om:
+            assert not gm.persistent
+            toks = np.random.default_rng(12).integers(3, host.cfg.n_vocab, 10)
+            for pos, t in enumerate(toks):
+                lg, ref = gm.forward(int(t), pos), om.forward(int(t), pos)
+                close(lg, ref, f"{variant} logits at position {pos}")
+                assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+                if pos in (0, 9):
+                    close(gm.layer_trace().reshape(-1), om.trace().reshape(-1), f"residual stream at {pos}")
+            k, v = gm.kv_read(host.cfg.n_layer - 1, 0, len(toks))
+            for pos in (0, 9):
+                kr, vr = om.kv(host.cfg.n_layer - 1, pos)
+                close(k[pos], kr, f"K row at {pos}")
+                close(v[pos], vr, f"V row at {pos}")
+            got = gm.generate_greedy(toks[:4].astype(np.uint32), 12)
+            assert np.array_equal(got, om.generate_greedy(toks[:4].astype(np.uint32), 12))
+
+
+def test_neox_rope_on_gated_block_matches_oracle():
+    """NEOX pairs on the llama block (config override): the per-phase step
+    rotates after the QKV projection; the persistent kernel steps aside."""
+    fw_cpu.set_threads(8)
+    with fwgpu.HostModel(synth=qwen2_q4(seed=23)) as host:
+        host.cfg.rope_type = 1
+        with fwgpu.GpuModel(host) as gm, fw_cpu.OracleModel(host) as om:
+            assert not gm.persistent
+            toks = np.random.default_rng(13).integers(3, host.cfg.n_vocab, 8)
+            for pos, t in enumerate(toks):
+                close(gm.forward(int(t), pos), om.forward(int(t), pos), f"logits at position {pos}")
+
+
+def test_phi2_fixture_prefill_and_greedy_match_reference():
+    """The phi2 prefill (token by token on the GPU) and the greedy loop after it
+    against the reference-generated fixture."""
+    name = "phi2"
+    gold = gold_model(name)
+    m = gs.MODELS[name]
+    prompt = gs.prompt(name)
+    f = len(prompt) - 1
+    with fwgpu.HostModel(synth=m["spec"](), max_ctx=m["max_ctx"]) as host, fwgpu.GpuModel(host) as gm:
+        lg = gm.prefill(prompt)
+        close(lg, gold[f"logits_{f}"], "prefill logits")
+        got = gm.generate_greedy_batched(prompt, m["n_gen"])
+    assert np.array_equal(got, gold["tokens"][len(prompt):])
