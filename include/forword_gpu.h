@@ -85,6 +85,11 @@ typedef struct forword_gpu forword_gpu_t;
  * max_ctx*(head_dim/2) floats (rope.c:6-17, transformer.c:73-89).
  * `max_ctx` is the already-resolved KV length (transformer.c:43-52).
  * Replaces the device-side half of transformer_init (transformer.c:14-128).
+ * Every block `model_config.c:148-217` describes runs except GPT-2's (no RoPE,
+ * fused attn_qkv, learned positions), which returns -1: RMSNorm or LayerNorm
+ * (with biases), sequential or parallel residual, gated or plain FFN with
+ * silu / gelu / gelu-tanh / relu, pairwise or NEOX RoPE, q/k/v and
+ * output-projection biases, an embedding scale, a head tied to token_embd.
  */
 int forword_gpu_init(forword_gpu_t **out,
                      const void *data, size_t data_size,

@@ -21,7 +21,11 @@
  *   fwc_rms_norm        test_runner.c:30-41 invariant, reference rms_norm bit-exact
  *   fwc_rope_apply      test_runner.c:60-90 (pos 0 identity), reference bit-exact
  *   fwc_softmax/attention/ffn/forward  reference transformer_forward bit-exact
- *                       (golden fixtures), per-layer residual stream
+ *                       (golden fixtures of the llama, qwen2, gemma and phi2
+ *                       blocks), per-layer residual stream
+ *   fwc_layer_norm      the phi2 fixture (bit-exact through the whole forward)
+ *   fwc_gelu_fast       the gemma and phi2 fixtures; float64 closed form
+ *   fwc_gelu            float64 closed form only (no fixture selects it)
  *   fwc_argmax          test_runner.c:93-96, tie and NaN rules
  */
 #ifndef FW_CPU_H
