@@ -89,7 +89,11 @@ hipError_t launch_dequant(const uint8_t *blocks, uint32_t type, uint64_t n_block
 
 // Split-K decode attention: partials [n_head][n_splits][head_dim + 2], then combine.
 uint32_t attn_splits(uint32_t max_ctx, uint32_t n_kv);
+// Attention kernels: head_dim 32/48/64/80/96/128/256, any GQA group (walked in
+// sub-groups of attn_sub_group query heads per workgroup).
 bool attn_supported(uint32_t head_dim, uint32_t group);
+uint32_t attn_epl(uint32_t head_dim);
+uint32_t attn_sub_group(uint32_t head_dim, uint32_t group);
 hipError_t launch_attention(const float *q, const float *kc, const float *vc, float *part, float *out,
                             uint32_t n_head, uint32_t n_kv, uint32_t head_dim, uint32_t n_splits,
                             const StepState *st, uint32_t pos_host, hipStream_t s);

@@ -493,16 +493,20 @@ hipError_t launch_dequant(const uint8_t *blocks, uint32_t type, uint64_t n_block
 
 // ── attention ────────────────────────────────────────────────────────────────
 
+// One workgroup: G query heads (of the group_total sharing KV head kvh; the
+// group is walked in n_sub = group_total / G workgroups) over one split of the
+// positions.
 template <int EPL, int G>
 __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ q, const float *__restrict__ kc,
                                                const float *__restrict__ vc, float *__restrict__ part,
                                                uint32_t n_kv, uint32_t n_splits, const StepState *st,
-                                               uint32_t pos_host, float scale_log2)
+                                               uint32_t pos_host, float scale_log2, uint32_t group_total)
 {
     constexpr int HD = 16 * EPL;
     __shared__ float s_m[4][G], s_l[4][G], s_o[4][G][HD];
     const uint32_t pos = st ? st->pos : pos_host;
-    const uint32_t kvh = blockIdx.x % n_kv, split = blockIdx.x / n_kv;
+    const uint32_t n_sub = group_total / G, kvh = blockIdx.x % n_kv, rest = blockIdx.x / n_kv;
+    const uint32_t sub = rest % n_sub, split = rest / n_sub, h0 = kvh * group_total + sub * G;
     const uint32_t n_pos = pos + 1, chunk = (n_pos + n_splits - 1) / n_splits;
     const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, l16 = lane & 15;
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ q, const
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < EPL; e++) qv[g][e] = q[(kvh * G + g) * HD + l16 * EPL + e];
+        for (int e = 0; e < EPL; e++) qv[g][e] = q[(h0 + g) * HD + l16 * EPL + e];
     float m[G], l[G], o[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -581,7 +585,7 @@ __global__ __launch_bounds__(256) void k_attn(const float *__restrict__ q, const
             L = __builtin_fmaf(s_l[w][g], c, L);
             O = __builtin_fmaf(s_o[w][g][dd], c, O);
         }
-        float *pp = part + ((size_t)(kvh * G + g) * n_splits + split) * (HD + 2);
+        float *pp = part + ((size_t)(h0 + g) * n_splits + split) * (HD + 2);
         pp[dd] = O;
         if (dd == 0) { pp[HD] = M; pp[HD + 1] = L; }
     }
@@ -625,23 +629,39 @@ uint32_t attn_splits(uint32_t max_ctx, uint32_t n_kv)
 
 bool attn_supported(uint32_t hd, uint32_t group)
 {
-    bool e = hd == 32 || hd == 48 || hd == 64 || hd == 128;
-    bool g = group == 1 || group == 2 || group == 4 || group == 8;
-    return e && g;
+    return attn_epl(hd) && group >= 1 && group <= 256;
+}
+
+uint32_t attn_epl(uint32_t hd)
+{
+    switch (hd) {
+    case 32: case 48: case 64: case 80: case 96: case 128: case 256: return hd / 16;
+    default: return 0;
+    }
+}
+
+uint32_t attn_sub_group(uint32_t hd, uint32_t group)
+{
+    for (uint32_t g = 8; g > 1; g >>= 1)
+        if (group % g == 0 && g * (hd / 16) <= 64) return g;   // q and o of G heads stay in registers
+    return 1;
 }
 
 template <int EPL>
-static hipError_t attn_g(uint32_t group, dim3 grid, hipStream_t s, const float *q, const float *kc,
-                         const float *vc, float *part, uint32_t n_kv, uint32_t ns, const StepState *st,
-                         uint32_t pos, float sc)
+static hipError_t attn_g(uint32_t group, uint32_t n_kv, uint32_t ns, hipStream_t s, const float *q,
+                         const float *kc, const float *vc, float *part, const StepState *st, uint32_t pos, float sc)
 {
-    switch (group) {
-    case 1: hipLaunchKernelGGL((k_attn<EPL, 1>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
-    case 2: hipLaunchKernelGGL((k_attn<EPL, 2>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
-    case 4: hipLaunchKernelGGL((k_attn<EPL, 4>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
-    case 8: hipLaunchKernelGGL((k_attn<EPL, 8>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc); break;
+    const uint32_t gs = attn_sub_group(16 * EPL, group);
+    const dim3 grid(n_kv * (group / gs) * ns);
+#define L(G) hipLaunchKernelGGL((k_attn<EPL, G>), grid, dim3(256), 0, s, q, kc, vc, part, n_kv, ns, st, pos, sc, group)
+    switch (gs) {
+    case 1: L(1); break;
+    case 2: L(2); break;
+    case 4: if constexpr (EPL <= 16) L(4); break;
+    case 8: if constexpr (EPL <= 8) L(8); break;
     default: return hipErrorInvalidValue;
     }
+#undef L
     return hipGetLastError();
 }
 
@@ -649,18 +669,23 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc, fl
                             uint32_t n_head, uint32_t n_kv, uint32_t hd, uint32_t n_splits,
                             const StepState *st, uint32_t pos_host, hipStream_t s)
 {
+    if (!n_kv || n_head % n_kv) return hipErrorInvalidValue;
     const uint32_t group = n_head / n_kv;
     // scores are dot * (1/sqrtf(hd)) (attention.c:143,151-155), carried in log2 units
     const float sc = (1.0f / sqrtf((float)hd)) * 1.4426950408889634f;
-    dim3 grid(n_kv * n_splits);
     hipError_t e;
+#define A(EPL) attn_g<EPL>(group, n_kv, n_splits, s, q, kc, vc, part, st, pos_host, sc)
     switch (hd) {
-    case 32: e = attn_g<2>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
-    case 48: e = attn_g<3>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
-    case 64: e = attn_g<4>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
-    case 128: e = attn_g<8>(group, grid, s, q, kc, vc, part, n_kv, n_splits, st, pos_host, sc); break;
+    case 32: e = A(2); break;
+    case 48: e = A(3); break;
+    case 64: e = A(4); break;
+    case 80: e = A(5); break;
+    case 96: e = A(6); break;
+    case 128: e = A(8); break;
+    case 256: e = A(16); break;
     default: return hipErrorInvalidValue;
     }
+#undef A
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(256), 0, s, part, out, n_splits, hd);
     return hipGetLastError();

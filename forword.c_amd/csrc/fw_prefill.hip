@@ -372,15 +372,18 @@ hipError_t launch_rope_append(float *qkv, const float *bias, uint32_t ld, uint32
 template <int EPL, int G>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ qkv, uint32_t ld,
                                                       const float *__restrict__ kc, const float *__restrict__ vc,
-                                                      float *__restrict__ out, uint32_t n_kv, uint32_t pos0)
+                                                      float *__restrict__ out, uint32_t n_kv, uint32_t pos0,
+                                                      uint32_t group_total)
 {
     constexpr int HD = 16 * EPL, NW = 4;
     __shared__ float s_o[NW][G][HD];
     __shared__ float s_m[NW][G], s_l[NW][G];
-    const uint32_t t = blockIdx.x, h = blockIdx.y, n_pos = pos0 + t + 1, kvd = n_kv * HD;
+    // G of the group_total query heads of KV head h (the group in n_sub workgroups)
+    const uint32_t n_sub = group_total / G, h = blockIdx.y / n_sub, h0 = h * group_total + (blockIdx.y % n_sub) * G;
+    const uint32_t t = blockIdx.x, n_pos = pos0 + t + 1, kvd = n_kv * HD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4, l16 = lane & 15;
     const float sc = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;      // attention.c:143, log2 units
-    const float *q = qkv + (size_t)t * ld + (size_t)h * G * HD;
+    const float *q = qkv + (size_t)t * ld + (size_t)h0 * HD;
     float qv[G][EPL], m[G], l[G], o[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -452,21 +455,25 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *__restrict__ 
             L = __builtin_fmaf(s_l[w][g], c, L);
             O = __builtin_fmaf(s_o[w][g][d], c, O);
         }
-        out[(size_t)t * (n_kv * G * HD) + ((size_t)h * G + g) * HD + d] = O / L;
+        out[(size_t)t * (n_kv * group_total * HD) + ((size_t)h0 + g) * HD + d] = O / L;
     }
 }
 
 template <int EPL>
-static hipError_t attn_prefill_g(uint32_t group, dim3 grid, hipStream_t s, const float *qkv, uint32_t ld,
+static hipError_t attn_prefill_g(uint32_t group, uint32_t n_tok, hipStream_t s, const float *qkv, uint32_t ld,
                                  const float *kc, const float *vc, float *out, uint32_t n_kv, uint32_t pos0)
 {
-    switch (group) {
-    case 1: hipLaunchKernelGGL((k_attn_prefill<EPL, 1>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
-    case 2: hipLaunchKernelGGL((k_attn_prefill<EPL, 2>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
-    case 4: hipLaunchKernelGGL((k_attn_prefill<EPL, 4>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
-    case 8: hipLaunchKernelGGL((k_attn_prefill<EPL, 8>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0); break;
+    const uint32_t gs = attn_sub_group(16 * EPL, group);
+    const dim3 grid(n_tok, n_kv * (group / gs));
+#define L(G) hipLaunchKernelGGL((k_attn_prefill<EPL, G>), grid, dim3(256), 0, s, qkv, ld, kc, vc, out, n_kv, pos0, group)
+    switch (gs) {
+    case 1: L(1); break;
+    case 2: L(2); break;
+    case 4: if constexpr (EPL <= 16) L(4); break;
+    case 8: if constexpr (EPL <= 8) L(8); break;
     default: return hipErrorNotSupported;
     }
+#undef L
     return hipGetLastError();
 }
 
@@ -475,15 +482,19 @@ hipError_t launch_attn_prefill(const float *qkv, uint32_t ld, uint32_t n_tok, co
                                uint32_t pos0, hipStream_t s)
 {
     if (!n_kv || n_head % n_kv) return hipErrorInvalidValue;
-    const dim3 grid(n_tok, n_kv);
     const uint32_t g = n_head / n_kv;
+#define A(EPL) attn_prefill_g<EPL>(g, n_tok, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0)
     switch (hd) {
-    case 32: return attn_prefill_g<2>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
-    case 48: return attn_prefill_g<3>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
-    case 64: return attn_prefill_g<4>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
-    case 128: return attn_prefill_g<8>(g, grid, s, qkv, ld, kc_layer, vc_layer, out, n_kv, pos0);
+    case 32: return A(2);
+    case 48: return A(3);
+    case 64: return A(4);
+    case 80: return A(5);
+    case 96: return A(6);
+    case 128: return A(8);
+    case 256: return A(16);
     default: return hipErrorNotSupported;
     }
+#undef A
 }
 
 } // namespace fw

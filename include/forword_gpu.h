@@ -90,6 +90,8 @@ typedef struct forword_gpu forword_gpu_t;
  * (with biases), sequential or parallel residual, gated or plain FFN with
  * silu / gelu / gelu-tanh / relu, pairwise or NEOX RoPE, q/k/v and
  * output-projection biases, an embedding scale, a head tied to token_embd.
+ * head_dim 32/48/64/80/96/128/256 with any GQA group; n_embd and n_ff
+ * multiples of the weight block (32 or 256 values).
  */
 int forword_gpu_init(forword_gpu_t **out,
                      const void *data, size_t data_size,

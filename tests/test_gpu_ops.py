@@ -218,7 +218,11 @@ def test_argmax_reference_cases(gold_ops):
 
 
 @pytest.mark.parametrize("cfg", [(6, 6, 48, 0), (6, 6, 48, 143), (8, 2, 32, 30), (32, 8, 128, 767),
-                                 (64, 8, 128, 382), (16, 8, 64, 1000), (32, 8, 128, 5000)],
+                                 (64, 8, 128, 382), (16, 8, 64, 1000), (32, 8, 128, 5000),
+                                 # head_dim 80/96/256 and groups 3/6/7/12 (phi-2, phi-3, gemma, qwen2 shapes)
+                                 (32, 32, 80, 300), (32, 32, 96, 200), (8, 1, 256, 150), (16, 16, 256, 90),
+                                 (14, 2, 64, 400), (12, 2, 128, 77), (28, 4, 128, 257), (12, 4, 96, 33),
+                                 (24, 2, 80, 64)],
                          ids=lambda c: "h{}_kv{}_hd{}_pos{}".format(*c))
 def test_attention_vs_oracle(cfg):
     n_head, n_kv, hd, pos = cfg

@@ -244,3 +244,34 @@ def test_phi2_fixture_prefill_and_greedy_match_reference():
         close(lg, gold[f"logits_{f}"], "prefill logits")
         got = gm.generate_greedy_batched(prompt, m["n_gen"])
     assert np.array_equal(got, gold["tokens"][len(prompt):])
+
+
+# Head dims and GQA groups of real checkpoints the persistent kernel does not
+# take (the per-phase step and the batched prefill run them): phi-2 hd 80,
+# phi-3 hd 96, gemma hd 256 (group 8), qwen2 groups 6 and 7.
+SHAPES_HD_GROUP = {
+    "llama_hd80_g1": (640, 1024, 2, 8, 8, 1000, "llama"),
+    "llama_hd96_g3": (1152, 1536, 2, 12, 4, 1000, "llama"),
+    "gemma_hd256_g8": (2048, 2048, 1, 8, 1, 1000, "gemma"),
+    "qwen2_hd64_g7": (896, 1536, 2, 14, 2, 1000, "qwen2"),
+    "qwen2_hd128_g6": (1536, 2048, 1, 12, 2, 1000, "qwen2"),
+    "phi2_hd80_g1": (640, 1024, 2, 8, 8, 1000, "phi2"),
+}
+
+
+@pytest.mark.parametrize("name", list(SHAPES_HD_GROUP))
+def test_head_dims_and_groups_match_oracle(name):
+    e, f, L, h, kv, v, arch = SHAPES_HD_GROUP[name]
+    fw_cpu.set_threads(8)
+    sp = fwgpu.spec(e, f, L, h, kv, v, 64, 10000.0, seed=51, arch=arch)
+    with fwgpu.HostModel(synth=sp) as host, fwgpu.GpuModel(host) as gm, fw_cpu.OracleModel(host) as om:
+        assert host.cfg.head_dim == e // h
+        toks = np.random.default_rng(14).integers(3, v, 20).astype(np.uint32)
+        for pos, t in enumerate(toks[:6]):
+            lg, ref = gm.forward(int(t), pos), om.forward(int(t), pos)
+            close(lg, ref, f"{name} logits at position {pos}")
+        lg = gm.prefill(toks)                       # batched where the block allows it
+        for pos, t in enumerate(toks):
+            ref = om.forward(int(t), pos)
+        close(lg, ref, f"{name} prefill logits")
+        assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
