@@ -475,8 +475,12 @@ static int setup_mk(forword_gpu_t *h)
     for (const Layer &Ly : h->L)
         for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })
             if (l->type != tl) return 0;
-    if (!mk_supported(n, c.n_ff, hd, c.n_head / c.n_head_kv, tl, h->out.type, h->embd.type) || c.n_head_kv + 1 > 64)
-        return 0;
+    // attention units: a KV head's query heads in power-of-two sub-groups (any group)
+    const uint32_t group = c.n_head / c.n_head_kv;
+    uint32_t gs = 8;
+    while (group % gs) gs >>= 1;
+    const uint32_t units = c.n_head_kv * (group / gs);
+    if (!mk_supported(n, c.n_ff, hd, group, tl, h->out.type, h->embd.type) || units + 1 > 64) return 0;
     int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 ||
@@ -498,8 +502,10 @@ static int setup_mk(forword_gpu_t *h)
     a.act = ffn_act_code(c);
     a.q = h->d_q; a.logits = h->d_logits; a.trace = h->d_trace;
     a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
-    // (KV head, split) attention items: about one per workgroup, >= 8 positions per split
-    uint32_t ns = (uint32_t)cus / c.n_head_kv;
+    // (attention unit, split) items: about one per workgroup, >= 8 positions per split
+    a.attn_gs = gs;
+    a.attn_units = units;
+    uint32_t ns = (uint32_t)cus / units;
     const uint32_t by_ctx = (uint32_t)((h->n_ctx + 7) / 8);
     if (ns > by_ctx) ns = by_ctx;
     if (ns > 256) ns = 256;

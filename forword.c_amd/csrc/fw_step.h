@@ -44,6 +44,9 @@ struct MkArgs {
     float embd_scale;
     uint32_t n_embd, n_ff, n_head, n_kv, head_dim, n_vocab, n_ctx, n_splits;
     uint32_t act;            // FfnAct of the gated FFN
+    // Attention units: the query heads of a KV head's group in sub-groups of
+    // attn_gs (a power of two dividing the group), attn_units = n_kv * group / attn_gs.
+    uint32_t attn_gs, attn_units;
     float eps;
     float *kc, *vc;
     const float *cos_tab, *sin_tab;

@@ -762,7 +762,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
         st_sys(a.am_v + blockIdx.x, bv);
         st_sys(a.am_i + blockIdx.x, bi);
         wait_mem();
-        s_last = ticket_sys(a.tickets + a.n_kv) == gridDim.x - 1;
+        s_last = ticket_sys(a.tickets + a.attn_units) == gridDim.x - 1;
     }
     __syncthreads();
     if (!s_last) return;
@@ -783,7 +783,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
             st_sys(&a.state->token, pos + 1 < n_prompt ? a.prompt[pos + 1] : r);
             st_sys(&a.state->pos, pos + 1);
         }
-        st_sys(a.tickets + a.n_kv, 0u);
+        st_sys(a.tickets + a.attn_units, 0u);
     }
 }
 
@@ -871,8 +871,10 @@ __device__ __forceinline__ void attn_batches(const FW_GLOBAL float *kc, const FW
 // (o[HD], m, l) per query head to a.part.  A position is spread over 32 lanes
 // (EPL = HD/32 dimensions each), so a wave walks two positions at a time.
 template <int EPL, int G>
-__device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint32_t pos, uint32_t kvh, uint32_t split, float *lds)
+__device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint32_t pos, uint32_t unit, uint32_t split, float *lds)
 {
+    const uint32_t n_sub = a.attn_units / a.n_kv, kvh = unit / n_sub;
+    const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * G;     // first query head of the unit
     constexpr int HD = 32 * EPL;
     float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
     float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
@@ -892,7 +894,7 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
         l[g] = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; e++) {
-            qv[g][e] = ld_sys(a.q + (kvh * G + g) * HD + l32 * EPL + e);
+            qv[g][e] = ld_sys(a.q + (h0 + g) * HD + l32 * EPL + e);
             o[g][e] = 0.f;
         }
     }
@@ -938,7 +940,7 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
             L = __builtin_fmaf(s_l[w][g], c, L);
             O = __builtin_fmaf(s_o[w][g][dd], c, O);
         }
-        float *pp = a.part + ((size_t)(kvh * G + g) * ns + split) * (HD + 2);
+        float *pp = a.part + ((size_t)(h0 + g) * ns + split) * (HD + 2);
         st_sys(pp + dd, O);
         if (dd == 0) { st_sys(pp + HD, M); st_sys(pp + HD + 1, L); }
     }
@@ -949,14 +951,16 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
 // Merge the splits of KV head kvh's G query heads into a.tatt (tagged): every split's
 // (m, l) in one batch of loads, then each thread's o values in batches of 32.
 template <int EPL, int G>
-__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, float *lds, uint32_t tag, uint32_t pos)
+__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t unit, float *lds, uint32_t tag, uint32_t pos)
 {
     constexpr int HD = 32 * EPL, SB = 32;
     const uint32_t ns = attn_splits_at(a, pos);
+    const uint32_t n_sub = a.attn_units / a.n_kv;
+    const uint32_t h0 = (unit / n_sub) * (a.n_head / a.n_kv) + (unit % n_sub) * G;
     float *s_w = lds;                                      // [G][ns] m, then the split weights
     float *s_l = lds + G * ns;                             // [G][ns] l
     float *s_inv = lds + 2 * G * ns;                       // [G] 1 / sum of weights
-    const float *base = a.part + (size_t)kvh * G * ns * (HD + 2);   // (head g, split s) at (g*ns + s)*(HD+2)
+    const float *base = a.part + (size_t)h0 * ns * (HD + 2);      // (head h0+g, split s) at (g*ns + s)*(HD+2)
     for (uint32_t t = tid(); t < G * ns; t += MK_THREADS) {
         const float2v ml = ld_sys2(base + (size_t)t * (HD + 2) + HD);
         s_w[t] = ml[0];
@@ -992,7 +996,7 @@ __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t kvh, floa
             for (int k = 0; k < SB; k++)
                 if (s0 + k < ns) O = __builtin_fmaf(v[k], w[s0 + k], O);
         }
-        st_sys64(a.tatt + (size_t)(kvh * G + g) * HD + d, tagged(O * s_inv[g], tag));
+        st_sys64(a.tatt + (size_t)(h0 + g) * HD + d, tagged(O * s_inv[g], tag));
     }
     __syncthreads();
 }
@@ -1001,15 +1005,15 @@ template <int EPL, int G>
 __device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
 {
     __shared__ uint32_t s_last;
-    const uint32_t items = a.n_kv * attn_splits_at(a, pos);
+    const uint32_t items = a.attn_units * attn_splits_at(a, pos);
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
-        const uint32_t kvh = it % a.n_kv, split = it / a.n_kv;
-        attn_item<EPL, G>(a, layer, pos, kvh, split, lds);
-        if (tid() == 0) s_last = ticket_sys(a.tickets + kvh) == attn_splits_at(a, pos) - 1;
+        const uint32_t unit = it % a.attn_units, split = it / a.attn_units;
+        attn_item<EPL, G>(a, layer, pos, unit, split, lds);
+        if (tid() == 0) s_last = ticket_sys(a.tickets + unit) == attn_splits_at(a, pos) - 1;
         __syncthreads();
         if (s_last) {
-            attn_combine<EPL, G>(a, kvh, lds, tag, pos);
-            if (tid() == 0) st_sys(a.tickets + kvh, 0u);
+            attn_combine<EPL, G>(a, unit, lds, tag, pos);
+            if (tid() == 0) st_sys(a.tickets + unit, 0u);
         }
     }
 }
@@ -1017,7 +1021,7 @@ __device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uin
 template <int EPL>
 __device__ __forceinline__ void attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
 {
-    switch (a.n_head / a.n_kv) {
+    switch (a.attn_gs) {
     case 1: attention_t<EPL, 1>(a, layer, pos, lds, tag); break;
     case 2: attention_t<EPL, 2>(a, layer, pos, lds, tag); break;
     case 4: attention_t<EPL, 4>(a, layer, pos, lds, tag); break;
@@ -1065,7 +1069,7 @@ __host__ __device__ inline uint32_t mk_fixed_floats(const MkArgs &a, uint32_t n_
 // Attention scratch (an item's per-wave partials, then the combine), from byte 0.
 __host__ __device__ inline uint32_t mk_attn_bytes(const MkArgs &a)
 {
-    const uint32_t G = a.n_head / a.n_kv;
+    const uint32_t G = a.attn_gs;
     const uint32_t item = MK_WAVES * G * a.head_dim + 2 * MK_WAVES * G, comb = 2 * G * a.n_splits + G;
     return ((item > comb ? item : comb) * 4 + 15) & ~15u;
 }
@@ -1240,7 +1244,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 // (not by a workgroup with an attention item: its KV loads
                 // would queue behind these DMAs)
                 const bool wrap = i + 1 == n_ops;
-                if (wrap ? step + 1 < a.n_steps : blockIdx.x >= a.n_kv * attn_splits_at(a, pos)) {
+                if (wrap ? step + 1 < a.n_steps : blockIdx.x >= a.attn_units * attn_splits_at(a, pos)) {
                     const uint32_t ni = wrap ? 0 : i + 2, nk = phase_kind(a, ni);   // past attention
                     const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
                     n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);        // WO, or the first QKV
@@ -1305,7 +1309,7 @@ bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t gr
 {
     if (n_embd % 64 || n_ff % 64 || n_embd / 64 > 64 * MK_SMAX || n_ff / 64 > 64 * MK_SMAX) return false;
     if (head_dim != 32 && head_dim != 64 && head_dim != 128) return false;
-    if (group != 1 && group != 2 && group != 4 && group != 8) return false;
+    if (group < 1) return false;                    // any group, in units of mk_attn_gs query heads
     return mk_type_ok(linear_type) && mk_type_ok(head_type) && (mk_type_ok(embd_type) || embd_type == kF32);
 }
 

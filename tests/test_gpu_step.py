@@ -3,7 +3,7 @@ transformer_forward steps, transformer.c:149-326, plus the greedy pick,
 sampler.c:28-32) against the oracle and against the per-phase kernels.
 
 Shapes cover every attention variant the kernel instantiates (head_dim 32 /
-64 / 128, GQA group 1 / 2 / 4 / 8), every weight type for the layer linears
+64 / 128, GQA group 1 / 2 / 4 / 8, and groups 3 / 6 / 7 walked in sub-groups), every weight type for the layer linears
 and the lm-head, column slices of 1..64 block pairs, and workgroups that own
 no rows.  Bar: logits and the residual stream within max-abs 2e-3 / rel 1e-3,
 identical greedy tokens."""
@@ -27,6 +27,10 @@ SHAPES = {
     "hd64_g8_q8": (1024, 2048, 2, 16, 2, 1536, 80, Q8, Q8, Q4),
     "hd32_g2_q4": (256, 768, 3, 8, 4, 1000, 160, Q4, Q4, Q5),
     "hd64_g1_wide": (256, 16448, 1, 4, 4, 512, 32, Q4, Q8, Q8),     # 257 pairs per down row: 64-pair slices
+    # groups that are not powers of two (qwen2 7B: 7, 1.5B: 6) split into sub-group units
+    "hd128_g7_q4": (1792, 2048, 2, 14, 2, 1000, 64, Q4, Q8, Q8),
+    "hd64_g6_q8": (768, 1536, 2, 12, 2, 1000, 64, Q8, Q8, Q8),
+    "hd64_g3_q5": (768, 1536, 2, 12, 4, 1000, 64, Q5, Q8, Q4),
 }
 
 
