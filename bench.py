@@ -88,7 +88,8 @@ def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34):
     """Algorithmic bytes of one token step at position pos: weights, embedding row, norm
     weights, KV read (rows 0..pos incl. the one just written) and KV write."""
     n, ff, L, hd, kv = cfg.n_embd, cfg.n_ff, cfg.n_layer, cfg.head_dim, cfg.n_head_kv
-    lin = L * ((n // 32) * linear_bb * (2 * n + 2 * kv * hd + 2 * ff) + (ff // 32) * linear_bb * n)
+    n_in = 2 if cfg.use_ffn_gate else 1                 # gate and up, or up alone
+    lin = L * ((n // 32) * linear_bb * (2 * n + 2 * kv * hd + n_in * ff) + (ff // 32) * linear_bb * n)
     head = (n // 32) * out_bb * cfg.n_vocab
     embd = (n // 32) * embd_bb
     norms = 4 * n * (2 * L + 1)
@@ -99,7 +100,8 @@ def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34):
 def linear_shapes(cfg):
     """(rows, cols) of every layer linear (q, k, v, o, gate, up, down)."""
     n, ff, kvd = cfg.n_embd, cfg.n_ff, cfg.n_head_kv * cfg.head_dim
-    return [(n, n), (kvd, n), (kvd, n), (n, n), (ff, n), (ff, n), (n, ff)] * cfg.n_layer
+    ffn = [(ff, n), (ff, n), (n, ff)] if cfg.use_ffn_gate else [(ff, n), (n, ff)]
+    return ([(n, n), (kvd, n), (kvd, n), (n, n)] + ffn) * cfg.n_layer
 
 
 def timed_decode(hip, gm, steps):
@@ -194,7 +196,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "tiny"])
+    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "qwen2-7b", "phi2", "tiny"])
     ap.add_argument("--mode", default="full", choices=["full", "decode", "copy"])
     ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -224,6 +226,12 @@ def main():
     elif args.config == "70b":
         sp = fwgpu.spec_70b(n_ctx=max(384, n_ctx))
         workload = "Llama-3-70B-shape Q4_0 greedy decode (Q8_0 embedding/output)"
+    elif args.config == "qwen2-7b":
+        sp = fwgpu.spec_qwen2_7b(n_ctx=max(768, n_ctx))
+        workload = "Qwen2-7B-shape Q4_0 greedy decode (q/k/v biases, GQA group 7; Q8_0 embedding/output)"
+    elif args.config == "phi2":
+        sp = fwgpu.spec_phi2(n_ctx=max(768, n_ctx))
+        workload = "Phi-2-shape Q4_0 greedy decode (LayerNorm, parallel residual, NEOX RoPE, hd 80)"
     else:
         sp = fwgpu.spec_tiny()
         sp.n_ctx = max(sp.n_ctx, n_ctx)

@@ -95,6 +95,20 @@ def spec_70b(seed=70, n_ctx=384, **kw):
     return spec(8192, 28672, 80, 64, 8, 128256, n_ctx, 500000.0, seed=seed, **kw)
 
 
+def spec_qwen2_7b(seed=27, n_ctx=768, **kw):
+    """Qwen2-7B shape: dim 3584, 28 layers, 28/4 heads (hd 128, group 7), ffn 18944, vocab
+    152064, q/k/v biases, RoPE base 1e6 (set by the config loader); Q4_0 linears."""
+    kw.setdefault("linear_type", GGML_Q4_0)
+    return spec(3584, 18944, 28, 28, 4, 152064, n_ctx, 1000000.0, seed=seed, arch="qwen2", **kw)
+
+
+def spec_phi2(seed=22, n_ctx=768, **kw):
+    """Phi-2 shape: dim 2560, 32 layers, 32/32 heads (hd 80), ffn 10240, vocab 51200, LayerNorm,
+    parallel residual, plain GELU FFN, NEOX RoPE; Q4_0 linears."""
+    kw.setdefault("linear_type", GGML_Q4_0)
+    return spec(2560, 10240, 32, 32, 32, 51200, n_ctx, 10000.0, seed=seed, arch="phi2", **kw)
+
+
 _host = None
 _gpu = None
 
