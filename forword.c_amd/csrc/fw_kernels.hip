@@ -152,6 +152,68 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
             for (int k = 0; k < R; k++)
                 if (ok[k]) acc[k] += dot_pair<T>(dw[k], xv, sx0, sx1);
         }
+    } else if constexpr (T == kQ4_K && PAIR) {
+        // 64-value quarters of dword-aligned super-blocks, one per lane at a time:
+        // groups 2p and 2p+1 share 32 code bytes (low and high nibbles), so each
+        // byte is loaded once.  Per group (d·sc)·Σq·x − (dmin·m)·Σx (quant.c:111-126
+        // factored; q in 1/512 units from the fp8 conversion, as for Q4_0).
+        const uint32_t n_pairs = a.n_cols / 64;
+        for (uint32_t u = lane; u < n_pairs; u += 64) {
+            float xv[64];
+            load_input<64>(a, 64 * (size_t)u, xv, xv4, nscale);
+            float sx0, sx1;
+            {
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
+                sx0 = s0 + s1;
+                sx1 = s2 + s3;
+            }
+            const uint32_t sb = u / 4, gp = u % 4;
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+                if (!ok[k]) continue;
+                const FW_GLOBAL uint32_t *b32 = gptr(reinterpret_cast<const uint32_t *>(wr[k] + (size_t)sb * 144));
+                const u32x4 hs = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(b32);   // d|dmin, scales 0..11
+                const float d = h2f(hs.x), dmin = h2f(hs.x >> 16);
+                const uint32_t sw[3] = { hs.y, hs.z, hs.w };
+                auto sb8 = [&](uint32_t i) { return (sw[i / 4] >> (8 * (i % 4))) & 0xFFu; };
+                float ds[2], dm[2];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t g = 2 * gp + h;
+                    uint32_t sc, mn;
+                    if (g < 4) { sc = sb8(g) & 63u; mn = sb8(g + 4) & 63u; }
+                    else {
+                        sc = (sb8(g + 4) & 15u) | ((sb8(g - 4) >> 6) << 4);
+                        mn = (sb8(g + 4) >> 4) | ((sb8(g) >> 6) << 4);
+                    }
+                    ds[h] = d * (float)sc;
+                    dm[h] = dmin * (float)mn;
+                }
+                const FW_GLOBAL uint32_t *q = b32 + 4 + gp * 8;
+                const u32x4 q0 = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(q);
+                const u32x4 q1 = *reinterpret_cast<const FW_GLOBAL u32x4_a4 *>(q + 4);
+                const uint32_t qw[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
+                float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t lo = qw[i] & 0x0F0F0F0Fu, hi = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                    const float2v l01 = nib2<false>(lo), l23 = nib2<true>(lo);
+                    const float2v h01 = nib2<false>(hi), h23 = nib2<true>(hi);
+                    a0 = __builtin_fmaf(l01.x, xv[4 * i + 0], a0);
+                    a1 = __builtin_fmaf(l01.y, xv[4 * i + 1], a1);
+                    a0 = __builtin_fmaf(l23.x, xv[4 * i + 2], a0);
+                    a1 = __builtin_fmaf(l23.y, xv[4 * i + 3], a1);
+                    b0 = __builtin_fmaf(h01.x, xv[32 + 4 * i + 0], b0);
+                    b1 = __builtin_fmaf(h01.y, xv[32 + 4 * i + 1], b1);
+                    b0 = __builtin_fmaf(h23.x, xv[32 + 4 * i + 2], b0);
+                    b1 = __builtin_fmaf(h23.y, xv[32 + 4 * i + 3], b1);
+                }
+                const float s0 = (a0 + a1) * 512.0f, s1 = (b0 + b1) * 512.0f;
+                acc[k] += __builtin_fmaf(ds[0], s0, -dm[0] * sx0) + __builtin_fmaf(ds[1], s1, -dm[1] * sx1);
+            }
+        }
     } else if constexpr (T == kQ4_K || T == kQ6_K) {
         // 32-value groups of the 256-value super-blocks, one per lane at a time:
         // the group's values exactly as the reference decodes them, then FMAs.

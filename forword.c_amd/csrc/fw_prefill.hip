@@ -24,6 +24,35 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // the result tile holds D[4·(l/16)+i][l%16] in element i of lane l.
 constexpr int PG_BM = 64, PG_BN = 128, PG_BK = 32, PG_THREADS = 256;
 
+// Values j0..j0+15 (j0 a multiple of 16) of a K super-block, each exactly as
+// dequant_q4_k / dequant_q6_k gives it, with the block's header decoded once
+// (quant.c:111-126, 160-183).
+template <uint32_t T>
+__device__ __forceinline__ void deq16_k(const uint8_t *blk, uint32_t j0, float (&w)[16])
+{
+    if constexpr (T == kQ4_K) {
+        const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const float dmin = h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+        const uint32_t g = j0 / 32;
+        uint32_t sc, mn;
+        scale_min_k4(g, blk + 4, sc, mn);
+        const float ds = d * (float)sc, dm = dmin * (float)mn;
+        const uint8_t *q = blk + 16 + (g / 2) * 32 + j0 % 32;
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = ds * (float)((g & 1) ? (q[i] >> 4) : (q[i] & 15)) - dm;
+    } else {
+        const uint32_t h = j0 / 128, r = j0 % 128, k = r / 32, l0 = r % 32;
+        const uint8_t *a = blk + h * 64 + l0 + 32 * (k & 1), *hb = blk + 128 + h * 32 + l0;
+        const int8_t sc = (int8_t)blk[192 + h * 8 + l0 / 16 + 2 * k];
+        const float ds = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8)) * (float)sc;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int q = (int)(((k >= 2) ? (a[i] >> 4) : (a[i] & 15)) | (((hb[i] >> (2 * k)) & 3) << 4));
+            w[i] = ds * (float)(q - 32);
+        }
+    }
+}
+
 template <uint32_t T>
 __global__ __launch_bounds__(PG_THREADS) void k_gemm_q(const float *__restrict__ X, uint32_t ldx,
                                                        const uint8_t *__restrict__ W, uint64_t row_bytes,
@@ -56,8 +85,15 @@ __global__ __launch_bounds__(PG_THREADS) void k_gemm_q(const float *__restrict__
         constexpr uint32_t BBY = T == kQ4_K ? 144u : T == kQ6_K ? 210u : T == kQ4_0 ? 18u : T == kQ5_0 ? 22u : 34u;
         const uint8_t *blk = wrow + (size_t)(k0 / BV) * BBY;
         const uint32_t j0 = k0 % BV + 16 * wh;
+        if constexpr (T == kQ4_K || T == kQ6_K) {
+            float w[16];
+            deq16_k<T>(blk, j0, w);                       // rows past n_out read row n_out-1 (wrow)
 #pragma unroll
-        for (int j = 0; j < 16; j++) Ws[wr][16 * wh + j] = r < n_out ? dequant_one(blk, T, j0 + j) : 0.f;
+            for (int j = 0; j < 16; j++) Ws[wr][16 * wh + j] = r < n_out ? w[j] : 0.f;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) Ws[wr][16 * wh + j] = r < n_out ? dequant_one(blk, T, j0 + j) : 0.f;
+        }
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < PG_BK; kk += 4) {
