@@ -108,8 +108,11 @@ hipError_t launch_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t head_
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s);
 // out = act(x) in place or not, FfnAct code (ffn.c:143-160, plain FFN).
 hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s);
-// layer_norm (norm.c:18-40) of one row of n floats; w and b may be null.
+// layer_norm (norm.c:18-40) of `rows` consecutive rows of n floats; w and b may be null.
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, uint32_t n, float eps,
+                            hipStream_t s, uint32_t rows = 1);
+// x += (a + bias[i % n]) + b2 over count floats (bias, b2 may be null).
+hipError_t launch_resid_add(float *x, const float *a, const float *bias, const float *b2, uint64_t count, uint32_t n,
                             hipStream_t s);
 // NEOX RoPE (rope.c:44-51) at the step's position: q heads in place and the K
 // cache row at pos of this layer.
@@ -158,7 +161,7 @@ hipError_t launch_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols, c
                              uint32_t n_tok, float embd_scale, float *x, hipStream_t s);
 // Rows [q | k | v] ld floats apart at positions pos0..: RoPE on q in place, K
 // (rotated) and V appended to the layer's cache rows.
-hipError_t launch_rope_append(float *qkv, const float *bias, uint32_t ld, uint32_t n_tok, uint32_t n_head,
+hipError_t launch_rope_append(float *qkv, const float *bias, int neox, uint32_t ld, uint32_t n_tok, uint32_t n_head,
                               uint32_t n_kv, uint32_t hd,
                               uint32_t pos0, const float *cos_tab, const float *sin_tab, float *kc_layer,
                               float *vc_layer, hipStream_t s);

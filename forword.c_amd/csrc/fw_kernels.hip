@@ -945,6 +945,8 @@ __global__ __launch_bounds__(1024) void k_layernorm(const float *__restrict__ x,
 {
     __shared__ double s[16];
     const uint32_t t = threadIdx.x;
+    x += (size_t)blockIdx.x * n;                  // one row per workgroup
+    out += (size_t)blockIdx.x * n;
     double acc = 0.0;
     for (uint32_t i = t; i < n; i += blockDim.x) acc += x[i];
     const float mean = (float)(block_sum_d(acc, s) / (double)n);
@@ -963,9 +965,29 @@ __global__ __launch_bounds__(1024) void k_layernorm(const float *__restrict__ x,
 }
 
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, uint32_t n, float eps,
+                            hipStream_t s, uint32_t rows)
+{
+    hipLaunchKernelGGL(k_layernorm, dim3(rows), dim3(1024), 0, s, x, w, b, out, n, eps);
+    return hipGetLastError();
+}
+
+// x[i] += (a[i] + bias[i % n]) + b2[i]: the residual add of a projection output
+// kept apart (its bias, and for a parallel block the FFN output), in the
+// reference's order (linear.c:214-221, transformer.c:250-251, 271-272).
+__global__ void k_resid_add(float *x, const float *a, const float *bias, const float *b2, uint64_t count, uint32_t n)
+{
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
+        float y = a[i];
+        if (bias) y += bias[i % n];
+        if (b2) y += b2[i];
+        x[i] += y;
+    }
+}
+
+hipError_t launch_resid_add(float *x, const float *a, const float *bias, const float *b2, uint64_t count, uint32_t n,
                             hipStream_t s)
 {
-    hipLaunchKernelGGL(k_layernorm, dim3(1), dim3(1024), 0, s, x, w, b, out, n, eps);
+    hipLaunchKernelGGL(k_resid_add, dim3(ew_blocks(count)), dim3(256), 0, s, x, a, bias, b2, count, n);
     return hipGetLastError();
 }
 

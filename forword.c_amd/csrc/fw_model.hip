@@ -235,11 +235,11 @@ static int bind_vec(forword_gpu_t *h, const float **p, const forword_gpu_tensor_
 
 // The block's pre-norm written out (transformer.c:234-239, 256-261, 275-280).
 static hipError_t launch_block_norm(const forword_gpu_t *h, const float *x, const float *w, const float *b, float *out,
-                                    hipStream_t s)
+                                    hipStream_t s, uint32_t rows = 1)
 {
     const forword_gpu_config_t &c = h->cfg;
-    if (c.norm_type == FORWORD_NORM_LAYER) return launch_layernorm(x, w, b, out, c.n_embd, c.norm_eps, s);
-    return launch_rmsnorm(x, w, out, c.n_embd, c.norm_eps, s);
+    if (c.norm_type == FORWORD_NORM_LAYER) return launch_layernorm(x, w, b, out, c.n_embd, c.norm_eps, s, rows);
+    return launch_rmsnorm_rows(x, w, out, c.n_embd, rows, c.norm_eps, s);
 }
 
 // One token step of any supported block (transformer.c:149-326): LayerNorm or
@@ -904,32 +904,26 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
     }
     for (size_t i = 0; i < n_tok; i++)
         if (tokens[i] >= c.n_vocab) { set_err("prefill: token %u out of range", tokens[i]); return -1; }
-    if (h->generic) {
-        // other blocks prefill token by token, as main.c:145-151 does; each step's
-        // state upload reads the pinned staging copy, so the host waits for the
-        // step before rewriting it
-        for (size_t i = 0; i < n_tok; i++) {
-            if (step_once(h, tokens[i], pos0 + i)) return -1;
-            HIPCHK(hipStreamSynchronize(h->stream), "prefill step");
-        }
-        return 0;
-    }
     const uint32_t n = c.n_embd, hd = c.head_dim, nq = c.n_head * hd, kvd = c.n_head_kv * hd, nff = c.n_ff;
     for (const Layer &Ly : h->L)
         for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })
-            if (!prefill_type_ok(l->type)) { set_err("prefill: linear type %u not supported", l->type); return -1; }
+            if ((l != &Ly.gate || c.use_ffn_gate) && !prefill_type_ok(l->type)) {
+                set_err("prefill: linear type %u not supported", l->type);
+                return -1;
+            }
     if (!attn_supported(hd, c.n_head / std::max<uint32_t>(c.n_head_kv, 1)) || c.n_head % c.n_head_kv || nq != n) {
         set_err("prefill: head layout not supported");
         return -1;
     }
-    // per-token activations: x, xn [n] | q k v [nq + 2 kvd] | attention [nq] | gate, up [n_ff]
-    const size_t ldqkv = (size_t)nq + 2 * kvd, per_tok = 2 * (size_t)n + ldqkv + nq + 2 * (size_t)nff;
+    // per-token activations: x, xn [n] | q k v [nq + 2 kvd] | attention [nq] | gate, up [n_ff] | attn_out [n]
+    const size_t ldqkv = (size_t)nq + 2 * kvd, per_tok = 3 * (size_t)n + ldqkv + nq + 2 * (size_t)nff;
     if (!h->d_pf && (dalloc(h, (void **)&h->d_pf, kPrefillChunk * per_tok * 4, "prefill activations") ||
                      dalloc(h, (void **)&h->d_pf_tok, kPrefillChunk * 4, "prefill tokens")))
         return -1;
     float *X = h->d_pf, *Xn = X + (size_t)kPrefillChunk * n, *QKV = Xn + (size_t)kPrefillChunk * n;
     float *Att = QKV + (size_t)kPrefillChunk * ldqkv, *G = Att + (size_t)kPrefillChunk * nq;
-    float *U = G + (size_t)kPrefillChunk * nff;
+    float *U = G + (size_t)kPrefillChunk * nff, *AO = U + (size_t)kPrefillChunk * nff;
+    const bool par = c.parallel_res != 0, neox = c.rope_type == FORWORD_ROPE_NEOX;
     hipStream_t s = h->stream;
 #define TRY(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { set_err("prefill: %s (line %d)", hipGetErrorString(e_), __LINE__); return -1; } } while (0)
     uint32_t rows = 0;
@@ -941,7 +935,7 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
         for (uint32_t l = 0; l < c.n_layer; l++) {
             const Layer &Ly = h->L[l];
             float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
-            TRY(launch_rmsnorm_rows(X, Ly.attn_norm, Xn, n, rows, c.norm_eps, s));            // transformer.c:255
+            TRY(launch_block_norm(h, X, Ly.attn_norm, Ly.attn_norm_b, Xn, s, rows));          // transformer.c:234-261
             if (Ly.q.type == Ly.k.type && Ly.k.type == Ly.v.type) {                           // q | k | v rows
                 GemmW g{};
                 g.w[0] = Ly.q.w; g.w[1] = Ly.k.w; g.w[2] = Ly.v.w;
@@ -954,19 +948,37 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
                 TRY(launch_gemm_q(Ly.v.type, Xn, n, Ly.v.w, Ly.v.row_bytes, QKV + nq + kvd, ldqkv, rows, kvd, n, false,
                                   s));
             }
-            TRY(launch_rope_append(QKV, Ly.bqkv, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
+            TRY(launch_rope_append(QKV, Ly.bqkv, neox, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
             TRY(launch_attn_prefill(QKV, ldqkv, rows, kc, vc, Att, c.n_head, c.n_head_kv, hd, p0, s));
-            TRY(launch_gemm_q(Ly.o.type, Att, nq, Ly.o.w, Ly.o.row_bytes, X, n, rows, n, nq, true, s));   // :271-272
-            TRY(launch_rmsnorm_rows(X, Ly.ffn_norm, Xn, n, rows, c.norm_eps, s));             // :275
-            TRY(launch_gemm_q(Ly.gate.type, Xn, n, Ly.gate.w, Ly.gate.row_bytes, G, nff, rows, nff, n, false, s));
-            TRY(launch_gemm_q(Ly.up.type, Xn, n, Ly.up.w, Ly.up.row_bytes, U, nff, rows, nff, n, false, s));
-            TRY(launch_act_mul(G, U, G, (uint64_t)rows * nff, ffn_act_code(c), s));           // ffn.c:88-103
-            TRY(launch_gemm_q(Ly.down.type, G, nff, Ly.down.w, Ly.down.row_bytes, X, n, rows, n, nff, true, s));
+            const uint64_t cnt = (uint64_t)rows * n;
+            if (par || Ly.bo) {                       // output projection kept apart: its bias, the parallel add
+                TRY(launch_gemm_q(Ly.o.type, Att, nq, Ly.o.w, Ly.o.row_bytes, AO, n, rows, n, nq, false, s));
+                if (!par) TRY(launch_resid_add(X, AO, Ly.bo, nullptr, cnt, n, s));         // :271-272
+            } else {
+                TRY(launch_gemm_q(Ly.o.type, Att, nq, Ly.o.w, Ly.o.row_bytes, X, n, rows, n, nq, true, s));   // :271-272
+            }
+            if (!par) TRY(launch_block_norm(h, X, Ly.ffn_norm, Ly.ffn_norm_b, Xn, s, rows));   // :275-280
+            const float *H = G;
+            if (c.use_ffn_gate) {                                                              // ffn.c:68-104
+                TRY(launch_gemm_q(Ly.gate.type, Xn, n, Ly.gate.w, Ly.gate.row_bytes, G, nff, rows, nff, n, false, s));
+                TRY(launch_gemm_q(Ly.up.type, Xn, n, Ly.up.w, Ly.up.row_bytes, U, nff, rows, nff, n, false, s));
+                TRY(launch_act_mul(G, U, G, (uint64_t)rows * nff, ffn_act_code(c), s));
+            } else {                                                                           // ffn.c:108-160
+                TRY(launch_gemm_q(Ly.up.type, Xn, n, Ly.up.w, Ly.up.row_bytes, U, nff, rows, nff, n, false, s));
+                TRY(launch_act(U, U, (uint64_t)rows * nff, plain_act_code(c), s));
+                H = U;
+            }
+            if (par) {                                                                         // transformer.c:250-251
+                TRY(launch_gemm_q(Ly.down.type, H, nff, Ly.down.w, Ly.down.row_bytes, Xn, n, rows, n, nff, false, s));
+                TRY(launch_resid_add(X, AO, Ly.bo, Xn, cnt, n, s));
+            } else {
+                TRY(launch_gemm_q(Ly.down.type, H, nff, Ly.down.w, Ly.down.row_bytes, X, n, rows, n, nff, true, s));
+            }
         }
     }
     // logits of the last token (transformer.c:293-323), then its argmax
     const float *xl = X + (size_t)(rows - 1) * n;
-    if (h->out_norm) TRY(launch_rmsnorm(xl, h->out_norm, h->d_xn, n, c.norm_eps, s));
+    if (h->out_norm) TRY(launch_block_norm(h, xl, h->out_norm, h->out_norm_b, h->d_xn, s));
     else TRY(hipMemcpyAsync(h->d_xn, xl, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
     {
         QmvArgs a{};

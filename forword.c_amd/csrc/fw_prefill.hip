@@ -357,8 +357,8 @@ hipError_t launch_embed_rows(const uint8_t *w, uint32_t type, uint32_t n_cols, c
 // add the bias of the same layout when there is one (linear.c:214-221), rotate
 // q in place and k (rope.c:37-43, interleaved pairs), append k and v to the
 // cache rows (attention.c:129-140).
-__global__ __launch_bounds__(256) void k_rope_append(float *qkv, const float *bias, uint32_t ld, uint32_t n_head,
-                                                     uint32_t n_kv, uint32_t hd, uint32_t pos0,
+__global__ __launch_bounds__(256) void k_rope_append(float *qkv, const float *bias, int neox, uint32_t ld,
+                                                     uint32_t n_head, uint32_t n_kv, uint32_t hd, uint32_t pos0,
                                                      const float *cos_tab, const float *sin_tab, float *kc, float *vc)
 {
     const uint32_t t = blockIdx.y, half = hd / 2, pos = pos0 + t, kvd = n_kv * hd;
@@ -367,17 +367,18 @@ __global__ __launch_bounds__(256) void k_rope_append(float *qkv, const float *bi
     const uint32_t n_pairs = (n_head + n_kv) * half;
     if (i < n_pairs) {
         const uint32_t p = i % half;
-        float *v = row + 2 * (size_t)i;          // pairs of q, then of k (contiguous)
+        // pair elements of q, then of k (contiguous): (2i, 2i+1), or NEOX (p, p + hd/2) of head i/half
+        const uint32_t e0 = neox ? (i / half) * hd + p : 2 * i, e1 = neox ? e0 + half : e0 + 1;
         const float c = cos_tab[(size_t)pos * half + p], s = sin_tab[(size_t)pos * half + p];
-        const float v0 = bias ? v[0] + bias[2 * i] : v[0], v1 = bias ? v[1] + bias[2 * i + 1] : v[1];
+        const float v0 = bias ? row[e0] + bias[e0] : row[e0], v1 = bias ? row[e1] + bias[e1] : row[e1];
         const float w0 = v0 * c - v1 * s, w1 = v0 * s + v1 * c;
         if (i < n_head * half) {
-            v[0] = w0;
-            v[1] = w1;
+            row[e0] = w0;
+            row[e1] = w1;
         } else {
-            const uint32_t e = 2 * (i - n_head * half);
-            kc[(size_t)pos * kvd + e] = w0;
-            kc[(size_t)pos * kvd + e + 1] = w1;
+            const uint32_t nq = n_head * hd;
+            kc[(size_t)pos * kvd + e0 - nq] = w0;
+            kc[(size_t)pos * kvd + e1 - nq] = w1;
         }
     } else if (i < n_pairs + kvd / 2) {
         const uint32_t e = 2 * (i - n_pairs);
@@ -387,13 +388,13 @@ __global__ __launch_bounds__(256) void k_rope_append(float *qkv, const float *bi
     }
 }
 
-hipError_t launch_rope_append(float *qkv, const float *bias, uint32_t ld, uint32_t n_tok, uint32_t n_head,
+hipError_t launch_rope_append(float *qkv, const float *bias, int neox, uint32_t ld, uint32_t n_tok, uint32_t n_head,
                               uint32_t n_kv, uint32_t hd,
                               uint32_t pos0, const float *cos_tab, const float *sin_tab, float *kc_layer,
                               float *vc_layer, hipStream_t s)
 {
     const uint32_t n = (n_head + n_kv) * (hd / 2) + n_kv * hd / 2;
-    hipLaunchKernelGGL(k_rope_append, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, bias, ld, n_head, n_kv, hd, pos0,
+    hipLaunchKernelGGL(k_rope_append, dim3((n + 255) / 256, n_tok), dim3(256), 0, s, qkv, bias, neox, ld, n_head, n_kv, hd, pos0,
                        cos_tab, sin_tab, kc_layer, vc_layer);
     return hipGetLastError();
 }

@@ -16,9 +16,8 @@ kernels by selecting it in the config.
 phi2: LayerNorm with biases (norm.c:18-40), parallel residual
 (transformer.c:232-252), plain FFN with the tanh GELU (ffn.c:108-171), NEOX
 RoPE (rope.c:44-51) and the output-projection bias (attention.c:106-107), on
-the explicit per-phase step (the persistent kernel and the batched prefill
-serve the RMSNorm / gated / sequential / pairwise-RoPE block only; a phi2
-prefill runs token by token).  Config overrides on the same file run the
+the explicit per-phase step (the persistent kernel serves the RMSNorm / gated /
+sequential / pairwise-RoPE block only) and in the batched prefill.  Config overrides on the same file run the
 remaining combinations: sequential LayerNorm, RMSNorm, pairwise RoPE, and the
 plain FFN's relu / silu / erf-GELU activations.
 
@@ -216,6 +215,17 @@ def test_phi2_family_matches_oracle(variant):
                 close(v[pos], vr, f"V row at {pos}")
             got = gm.generate_greedy(toks[:4].astype(np.uint32), 12)
             assert np.array_equal(got, om.generate_greedy(toks[:4].astype(np.uint32), 12))
+            # batched prefill of the same block: last logits and KV rows
+            prompt = np.random.default_rng(15).integers(3, host.cfg.n_vocab, 33).astype(np.uint32)
+            lg = gm.prefill(prompt)
+            for pos, t in enumerate(prompt):
+                ref = om.forward(int(t), pos)
+            close(lg, ref, f"{variant} prefill logits")
+            k, v = gm.kv_read(0, 0, len(prompt))
+            for pos in (0, 32):
+                kr, vr = om.kv(0, pos)
+                close(k[pos], kr, f"prefill K row at {pos}")
+                close(v[pos], vr, f"prefill V row at {pos}")
 
 
 def test_neox_rope_on_gated_block_matches_oracle():
@@ -232,8 +242,8 @@ def test_neox_rope_on_gated_block_matches_oracle():
 
 
 def test_phi2_fixture_prefill_and_greedy_match_reference():
-    """The phi2 prefill (token by token on the GPU) and the greedy loop after it
-    against the reference-generated fixture."""
+    """The phi2 batched prefill and the greedy loop after it against the
+    reference-generated fixture."""
     name = "phi2"
     gold = gold_model(name)
     m = gs.MODELS[name]
