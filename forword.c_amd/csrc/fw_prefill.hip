@@ -180,12 +180,41 @@ __device__ __forceinline__ void deq_pair_block(const uint32_t *dw, int b, float 
 // current one.  Needs n_in % 64 == 0 (so rows are dword aligned).
 constexpr int PP_BK = 64, PP_XS = PP_BK + 4;
 
+// Dwords one thread pair loads per 64 columns: a block pair, or for Q4_K the
+// super-block header (4 dwords) and the quarter's 32 code bytes (8 dwords).
+template <uint32_t T> constexpr int pair_dwords()
+{
+    if constexpr (T == kQ4_K) return 12;
+    else return Blk<T>::pair_dw;
+}
+
+// Group 2·gp + hb (hb = 0: low nibbles, 1: high) of a Q4_K super-block quarter
+// loaded as header + code dwords, each value exactly as dequant_q4_k gives it.
+__device__ __forceinline__ void deq_q4k_half(const uint32_t *wd, uint32_t gp, int hb, float (&w)[32])
+{
+    const float d = h2f(wd[0]), dmin = h2f(wd[0] >> 16);
+    auto sb8 = [&](uint32_t i) { return (wd[1 + i / 4] >> (8 * (i % 4))) & 0xFFu; };
+    const uint32_t g = 2 * gp + (uint32_t)hb;
+    uint32_t sc, mn;
+    if (g < 4) { sc = sb8(g) & 63u; mn = sb8(g + 4) & 63u; }
+    else {
+        sc = (sb8(g + 4) & 15u) | ((sb8(g - 4) >> 6) << 4);
+        mn = (sb8(g + 4) >> 4) | ((sb8(g) >> 6) << 4);
+    }
+    const float ds = d * (float)sc, dm = dmin * (float)mn;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const uint32_t b = (wd[4 + i / 4] >> (8 * (i % 4))) & 0xFFu;
+        w[i] = ds * (float)(hb ? (b >> 4) : (b & 15u)) - dm;
+    }
+}
+
 template <uint32_t T>
 __global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict__ X, uint32_t ldx, GemmW g,
                                                         float *__restrict__ Y, uint32_t ldy, uint32_t n_tok,
                                                         uint32_t n_in, int accumulate)
 {
-    constexpr int PDW = Blk<T>::pair_dw, XV = PG_BM * PP_BK / 4 / PG_THREADS;   // float4 of x per thread
+    constexpr int PDW = pair_dwords<T>(), XV = PG_BM * PP_BK / 4 / PG_THREADS;   // float4 of x per thread
     __shared__ __align__(16) float Xs[PG_BM][PP_XS];
     __shared__ __align__(16) float Ws[PG_BN][PP_XS];
     const uint32_t r0 = blockIdx.x * PG_BN, t0 = blockIdx.y * PG_BM;
@@ -218,7 +247,16 @@ __global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict_
             xr[i] = t < n_tok ? *reinterpret_cast<const float4 *>(X + (size_t)t * ldx + k0 + 4 * c4)
                               : float4{0.f, 0.f, 0.f, 0.f};
         }
-        load_pair<T>(wrow + (size_t)(k0 / 64) * (2 * Blk<T>::bytes), wd);
+        if constexpr (T == kQ4_K) {
+            const uint32_t c = k0 / 64;
+            const uint32_t *b32 = reinterpret_cast<const uint32_t *>(wrow + (size_t)(c / 4) * 144);
+#pragma unroll
+            for (int i = 0; i < 4; i++) wd[i] = b32[i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) wd[4 + i] = b32[4 + (c % 4) * 8 + i];
+        } else {
+            load_pair<T>(wrow + (size_t)(k0 / 64) * (2 * Blk<T>::bytes), wd);
+        }
     };
     fetch(0);
     for (uint32_t k0 = 0; k0 < n_in; k0 += PP_BK) {
@@ -229,7 +267,8 @@ __global__ __launch_bounds__(PG_THREADS) void k_gemm_qp(const float *__restrict_
         }
         {
             float w[32];
-            deq_pair_block<T>(wd, wb, w);
+            if constexpr (T == kQ4_K) deq_q4k_half(wd, (k0 / 64) % 4, wb, w);
+            else deq_pair_block<T>(wd, wb, w);
 #pragma unroll
             for (int j = 0; j < 32; j += 4)
                 *reinterpret_cast<float4 *>(&Ws[wr][32 * wb + j]) =
@@ -285,8 +324,9 @@ hipError_t launch_gemm_qs(uint32_t type, const float *x, uint32_t ldx, const Gem
     const int acc = accumulate ? 1 : 0;
     // block pairs when rows are whole pairs at dword-aligned addresses, x rows float4 aligned and
     // every matrix starts on a tile boundary; else one launch of the general kernel per matrix
-    bool pairs = (type == kQ4_0 || type == kQ5_0 || type == kQ8_0) && n_in % 64 == 0 && ((uintptr_t)x & 15) == 0 &&
-                 ldx % 4 == 0;
+    bool pairs = (type == kQ4_0 || type == kQ5_0 || type == kQ8_0 || type == kQ4_K) && n_in % 64 == 0 &&
+                 ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
+    for (uint32_t i = 0; i < g.n_seg; i++) pairs = pairs && g.rb[i] % 4 == 0;     // every row dword-aligned
     for (uint32_t i = 0; i < g.n_seg; i++) {
         pairs = pairs && ((uintptr_t)g.w[i] & 3) == 0;
         if (i + 1 < g.n_seg) pairs = pairs && g.end[i] % PG_BN == 0;
@@ -298,6 +338,7 @@ hipError_t launch_gemm_qs(uint32_t type, const float *x, uint32_t ldx, const Gem
         case kQ4_0: GEMM(kQ4_0); break;
         case kQ5_0: GEMM(kQ5_0); break;
         case kQ8_0: GEMM(kQ8_0); break;
+        case kQ4_K: GEMM(kQ4_K); break;
         default: return hipErrorNotSupported;
         }
 #undef GEMM
