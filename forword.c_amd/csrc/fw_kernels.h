@@ -106,8 +106,13 @@ uint32_t argmax_blocks(uint32_t n);
 hipError_t launch_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t head_dim, const float *cos_tab,
                        const float *sin_tab, int neox, hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s);
-// out = act(x) in place or not, FfnAct code (ffn.c:143-160, plain FFN).
-hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s);
+// out = act(x + bias[i % period]) in place or not, FfnAct code (ffn.c:143-160, plain FFN;
+// the bias is GPT-2's ffn_up.bias, may be null).
+hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s,
+                      const float *bias = nullptr, uint32_t period = 1);
+// x[r] += position-embedding row (st ? st->pos : p0) + r, r < rows (transformer.c:188-205).
+hipError_t launch_pos_add(const uint8_t *w, uint32_t type, uint64_t row_bytes, uint32_t n, const StepState *st,
+                          uint32_t p0, uint32_t rows, float *x, hipStream_t s);
 // layer_norm (norm.c:18-40) of `rows` consecutive rows of n floats; w and b may be null.
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, uint32_t n, float eps,
                             hipStream_t s, uint32_t rows = 1);

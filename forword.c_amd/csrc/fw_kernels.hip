@@ -911,15 +911,41 @@ hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t 
     return hipGetLastError();
 }
 
-__global__ void k_act(const float *x, float *out, uint64_t n, uint32_t act)
+__global__ void k_act(const float *x, float *out, uint64_t n, uint32_t act, const float *bias, uint32_t period)
 {
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
-        out[i] = ffn_act(x[i], act);
+        out[i] = ffn_act(bias ? x[i] + bias[i % period] : x[i], act);
 }
 
-hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s)
+hipError_t launch_act(const float *x, float *out, uint64_t n, uint32_t act, hipStream_t s, const float *bias,
+                      uint32_t period)
 {
-    hipLaunchKernelGGL(k_act, dim3(ew_blocks(n)), dim3(256), 0, s, x, out, n, act);
+    hipLaunchKernelGGL(k_act, dim3(ew_blocks(n)), dim3(256), 0, s, x, out, n, act, bias, period);
+    return hipGetLastError();
+}
+
+// x[r] += row (pos + r) of a position-embedding table (transformer.c:188-205),
+// pos from the step state or p0; rows decoded exactly (linear_get_row).
+__global__ void k_pos_add(const uint8_t *w, uint32_t type, uint64_t row_bytes, uint32_t n, const StepState *st,
+                          uint32_t p0, float *x)
+{
+    const uint32_t r = blockIdx.y, row = (st ? st->pos : p0) + r;
+    const uint8_t *wr = w + (size_t)row * row_bytes;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float v;
+        if (type == kF32) v = reinterpret_cast<const float *>(wr)[i];
+        else {
+            const uint32_t bv = block_values_dev(type);
+            v = dequant_one(wr + (size_t)(i / bv) * block_bytes_dev(type), type, i % bv);
+        }
+        x[(size_t)r * n + i] += v;
+    }
+}
+
+hipError_t launch_pos_add(const uint8_t *w, uint32_t type, uint64_t row_bytes, uint32_t n, const StepState *st,
+                          uint32_t p0, uint32_t rows, float *x, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_pos_add, dim3((n + 255) / 256, rows), dim3(256), 0, s, w, type, row_bytes, n, st, p0, x);
     return hipGetLastError();
 }
 

@@ -63,6 +63,7 @@ struct Layer {
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
     const float *attn_norm_b = nullptr, *ffn_norm_b = nullptr;   // LayerNorm biases, or null
     const float *bo = nullptr;     // attn_output.bias, or null
+    const float *bu = nullptr, *bd = nullptr;   // GPT-2 ffn_up.bias / ffn_down.bias, or null
     const float *bqkv = nullptr;   // attn_q|k|v.bias concatenated [n_embd + 2 kv_dim] (qwen2), or null
     Lin q, k, v, o, gate, up, down;
 };
@@ -128,6 +129,7 @@ struct forword_gpu {
     float *d_pss = nullptr, *d_scale = nullptr;      // RMSNorm scale published by the residual kernels
     float *d_bias = nullptr;                         // per-layer q|k|v biases (qwen2)
     const float *out_norm_b = nullptr;               // output_norm.bias (LayerNorm), or null
+    Lin pos_embd;                                    // GPT-2 learned positions (w null otherwise)
     // Blocks other than the RMSNorm / gated-FFN / sequential / pairwise-RoPE one
     // (LayerNorm, parallel residual, plain FFN, NEOX RoPE, output-projection
     // bias) run the explicit per-phase step (enqueue_step_generic).
@@ -255,6 +257,9 @@ static hipError_t enqueue_step_generic(forword_gpu_t *h)
 #define TRY(x) do { e = (x); if (e != hipSuccess) return e; } while (0)
     TRY(launch_embed(h->embd.w, h->embd.type, n, h->embd.out, h->d_state, nullptr, c.embd_scale, h->d_x,
                      h->d_scale, c.norm_eps, s));                                       // transformer.c:167-182
+    if (h->pos_embd.w)                                                                  // transformer.c:188-205
+        TRY(launch_pos_add(h->pos_embd.w, h->pos_embd.type, h->pos_embd.row_bytes, n, h->d_state, 0, 1, h->d_x, s));
+    const bool rope = c.rope_type != FORWORD_ROPE_NONE;
     for (uint32_t l = 0; l < c.n_layer; l++) {
         const Layer &Ly = h->L[l];
         float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
@@ -270,7 +275,7 @@ static hipError_t enqueue_step_generic(forword_gpu_t *h)
             a.row_bytes = qkv[s0]->row_bytes;
             a.x = h->d_xn;
             a.out[0] = h->d_q; a.out[1] = kc; a.out[2] = vc;
-            if (!neox) { a.cos_tab = h->d_cos; a.sin_tab = h->d_sin; }
+            if (rope && !neox) { a.cos_tab = h->d_cos; a.sin_tab = h->d_sin; }
             if (Ly.bqkv) { a.bias[0] = Ly.bqkv; a.bias[1] = Ly.bqkv + n; a.bias[2] = Ly.bqkv + n + kvd; }
             a.state = h->d_state;
             a.head_dim = hd;
@@ -278,7 +283,7 @@ static hipError_t enqueue_step_generic(forword_gpu_t *h)
             qmv_plan(a, EPI_QKV);
             TRY(launch_qmv(qkv[s0]->type, EPI_QKV, a, s));
         }
-        if (neox) TRY(launch_rope_neox_step(h->d_q, kc, c.n_head, c.n_head_kv, hd, h->d_cos, h->d_sin, h->d_state, s));
+        if (rope && neox) TRY(launch_rope_neox_step(h->d_q, kc, c.n_head, c.n_head_kv, hd, h->d_cos, h->d_sin, h->d_state, s));
         TRY(launch_attention(h->d_q, kc, vc, h->d_part, h->d_att, c.n_head, c.n_head_kv, hd, h->n_splits,
                              h->d_state, 0, s));                                        // attention.c:142-164
         {
@@ -306,7 +311,7 @@ static hipError_t enqueue_step_generic(forword_gpu_t *h)
         } else {                                                                        // ffn.c:108-160
             QmvArgs a{};
             a.n_seg = 1; a.w[0] = Ly.up.w; a.rows[0] = c.n_ff; a.n_cols = n; a.row_bytes = Ly.up.row_bytes;
-            a.x = h->d_xn; a.out[0] = h->d_h;
+            a.x = h->d_xn; a.out[0] = h->d_h; a.bias[0] = Ly.bu;
             qmv_plan(a, EPI_STORE);
             TRY(launch_qmv(Ly.up.type, EPI_STORE, a, s));
             TRY(launch_act(h->d_h, h->d_h, c.n_ff, plain_act_code(c), s));
@@ -315,6 +320,7 @@ static hipError_t enqueue_step_generic(forword_gpu_t *h)
             QmvArgs a{};                                                                // ffn.c:106/168, transformer.c:250/287
             a.n_seg = 1; a.w[0] = Ly.down.w; a.rows[0] = n; a.n_cols = c.n_ff; a.row_bytes = Ly.down.row_bytes;
             a.x = h->d_h; a.out[0] = h->d_x; a.trace = h->d_trace + (size_t)(2 * l + 1) * n;
+            a.bias[0] = Ly.bd;
             if (par) { a.addend = h->d_ao; a.trace2 = h->d_trace + (size_t)(2 * l) * n; }
             qmv_plan(a, EPI_RESID);
             TRY(launch_qmv(Ly.down.type, EPI_RESID, a, s));
@@ -620,10 +626,10 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         set_err("forword_gpu_init: invalid model dimensions");
         return -1;
     }
-    if ((c.norm_type != FORWORD_NORM_RMS && c.norm_type != FORWORD_NORM_LAYER) || c.arch == FORWORD_ARCH_GPT2 ||
-        (c.rope_type != FORWORD_ROPE_NORMAL && c.rope_type != FORWORD_ROPE_NEOX)) {
-        set_err("forword_gpu_init: GPT-2 style blocks (fused QKV, learned positions, no RoPE) and unknown "
-                "norm/RoPE types are not implemented");
+    if ((c.norm_type != FORWORD_NORM_RMS && c.norm_type != FORWORD_NORM_LAYER) ||
+        (c.rope_type != FORWORD_ROPE_NORMAL && c.rope_type != FORWORD_ROPE_NEOX && c.rope_type != FORWORD_ROPE_NONE) ||
+        (c.arch == FORWORD_ARCH_GPT2 && c.n_head_kv != c.n_head)) {
+        set_err("forword_gpu_init: unknown norm or RoPE type, or a GPT-2 model with grouped KV heads");
         return -1;
     }
     if (!attn_supported(c.head_dim, c.n_head / c.n_head_kv)) {
@@ -669,9 +675,19 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
 #define LIN(f, sfx, in_, out_)                                                          \
         snprintf(nm, sizeof nm, "blk.%u." sfx, l);                                      \
         if (bind_lin(h, Ly.f, find_t(tensors, n_tensors, nm), nm, in_, out_)) FAIL();
-        LIN(q, "attn_q.weight", n, n);
-        LIN(k, "attn_k.weight", n, kvd);
-        LIN(v, "attn_v.weight", n, kvd);
+        if (c.arch == FORWORD_ARCH_GPT2) {          // one [q | k | v] projection (attention.c:68-96)
+            Lin qkv;
+            LIN(q, "attn_qkv.weight", n, 3 * n);
+            qkv = Ly.q;
+            Ly.q.out = Ly.k.out = Ly.v.out = n;
+            Ly.k = Ly.q; Ly.v = Ly.q;
+            Ly.k.w = qkv.w + (size_t)n * qkv.row_bytes;
+            Ly.v.w = qkv.w + 2 * (size_t)n * qkv.row_bytes;
+        } else {
+            LIN(q, "attn_q.weight", n, n);
+            LIN(k, "attn_k.weight", n, kvd);
+            LIN(v, "attn_v.weight", n, kvd);
+        }
         LIN(o, "attn_output.weight", n, n);
         if (c.use_ffn_gate) {
             LIN(gate, "ffn_gate.weight", n, c.n_ff);
@@ -687,6 +703,14 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
             const forword_gpu_tensor_t *td = find_t(tensors, n_tensors, nm);
             if (!td) { snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); td = find_t(tensors, n_tensors, nm); }
             if (bind_lin(h, Ly.down, td, nm, c.n_ff, n)) FAIL();
+            if (c.arch == FORWORD_ARCH_GPT2) {      // ffn.c:127-140 (required), :162-166 (fc2 has none)
+                const bool fc2 = strstr(nm, "fc2") != nullptr;
+                snprintf(nm, sizeof nm, "blk.%u.ffn_up.bias", l);
+                if (bind_vec(h, &Ly.bu, find_t(tensors, n_tensors, nm), nm, c.n_ff, true)) FAIL();
+                snprintf(nm, sizeof nm, "blk.%u.ffn_down.bias", l);
+                if (bind_vec(h, &Ly.bd, find_t(tensors, n_tensors, nm), nm, n, true)) FAIL();
+                if (fc2) Ly.bd = nullptr;
+            }
         }
 #undef LIN
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l);
@@ -703,8 +727,23 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
     }
     if (c.norm_type != FORWORD_NORM_RMS || c.parallel_res || !c.use_ffn_gate || c.rope_type != FORWORD_ROPE_NORMAL)
         h->generic = true;
+    if (c.arch == FORWORD_ARCH_GPT2) {                                                  // transformer.c:188-205
+        const forword_gpu_tensor_t *tp = find_t(tensors, n_tensors, "position_embd.weight");
+        if (bind_lin(h, h->pos_embd, tp, "position_embd.weight", n, tp && tp->n_dims > 1 ? tp->dims[1] : 0)) FAIL();
+        if (h->pos_embd.out < max_ctx) {
+            set_err("position_embd.weight has %u rows, fewer than the %zu positions", h->pos_embd.out, max_ctx);
+            FAIL();
+        }
+    }
     if (c.parallel_res && dalloc(h, (void **)&h->d_ao, (size_t)n * 4, "attention output")) FAIL();
-    if (c.use_qkv_bias) {
+    if (c.arch == FORWORD_ARCH_GPT2) {
+        // attention.c:78-90: attn_qkv.bias is already [q | k | v], used in place
+        for (uint32_t l = 0; l < c.n_layer; l++) {
+            char nm[96];
+            snprintf(nm, sizeof nm, "blk.%u.attn_qkv.bias", l);
+            if (bind_vec(h, &h->L[l].bqkv, find_t(tensors, n_tensors, nm), nm, 3 * (size_t)n, false)) FAIL();
+        }
+    } else if (c.use_qkv_bias) {
         // attention.c:114-122: the q/k/v biases of each layer, gathered into one
         // [n_embd | kv_dim | kv_dim] vector in the order the fused QKV rows use;
         // a missing one adds nothing (zeros).  linear.c:214-221 adds F32 biases only.
@@ -932,6 +971,8 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
         const uint32_t p0 = (uint32_t)(pos0 + c0);
         TRY(hipMemcpyAsync(h->d_pf_tok, tokens + c0, (size_t)rows * 4, hipMemcpyHostToDevice, s));
         TRY(launch_embed_rows(h->embd.w, h->embd.type, n, h->d_pf_tok, rows, c.embd_scale, X, s));
+        if (h->pos_embd.w)                                                              // transformer.c:188-205
+            TRY(launch_pos_add(h->pos_embd.w, h->pos_embd.type, h->pos_embd.row_bytes, n, nullptr, p0, rows, X, s));
         for (uint32_t l = 0; l < c.n_layer; l++) {
             const Layer &Ly = h->L[l];
             float *kc = h->d_k + (size_t)l * h->n_ctx * kvd, *vc = h->d_v + (size_t)l * h->n_ctx * kvd;
@@ -948,7 +989,7 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
                 TRY(launch_gemm_q(Ly.v.type, Xn, n, Ly.v.w, Ly.v.row_bytes, QKV + nq + kvd, ldqkv, rows, kvd, n, false,
                                   s));
             }
-            TRY(launch_rope_append(QKV, Ly.bqkv, neox, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
+            TRY(launch_rope_append(QKV, Ly.bqkv, c.rope_type == FORWORD_ROPE_NONE ? 2 : neox ? 1 : 0, ldqkv, rows, c.n_head, c.n_head_kv, hd, p0, h->d_cos, h->d_sin, kc, vc, s));
             TRY(launch_attn_prefill(QKV, ldqkv, rows, kc, vc, Att, c.n_head, c.n_head_kv, hd, p0, s));
             const uint64_t cnt = (uint64_t)rows * n;
             if (par || Ly.bo) {                       // output projection kept apart: its bias, the parallel add
@@ -965,12 +1006,15 @@ static int prefill_run(forword_gpu_t *h, const uint32_t *tokens, size_t n_tok, s
                 TRY(launch_act_mul(G, U, G, (uint64_t)rows * nff, ffn_act_code(c), s));
             } else {                                                                           // ffn.c:108-160
                 TRY(launch_gemm_q(Ly.up.type, Xn, n, Ly.up.w, Ly.up.row_bytes, U, nff, rows, nff, n, false, s));
-                TRY(launch_act(U, U, (uint64_t)rows * nff, plain_act_code(c), s));
+                TRY(launch_act(U, U, (uint64_t)rows * nff, plain_act_code(c), s, Ly.bu, nff));
                 H = U;
             }
             if (par) {                                                                         // transformer.c:250-251
                 TRY(launch_gemm_q(Ly.down.type, H, nff, Ly.down.w, Ly.down.row_bytes, Xn, n, rows, n, nff, false, s));
                 TRY(launch_resid_add(X, AO, Ly.bo, Xn, cnt, n, s));
+            } else if (Ly.bd) {                                                                // x += (W h + bd)
+                TRY(launch_gemm_q(Ly.down.type, H, nff, Ly.down.w, Ly.down.row_bytes, AO, n, rows, n, nff, false, s));
+                TRY(launch_resid_add(X, AO, Ly.bd, nullptr, cnt, n, s));
             } else {
                 TRY(launch_gemm_q(Ly.down.type, H, nff, Ly.down.w, Ly.down.row_bytes, X, n, rows, n, nff, true, s));
             }

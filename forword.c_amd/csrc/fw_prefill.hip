@@ -412,7 +412,8 @@ __global__ __launch_bounds__(256) void k_rope_append(float *qkv, const float *bi
         const uint32_t e0 = neox ? (i / half) * hd + p : 2 * i, e1 = neox ? e0 + half : e0 + 1;
         const float c = cos_tab[(size_t)pos * half + p], s = sin_tab[(size_t)pos * half + p];
         const float v0 = bias ? row[e0] + bias[e0] : row[e0], v1 = bias ? row[e1] + bias[e1] : row[e1];
-        const float w0 = v0 * c - v1 * s, w1 = v0 * s + v1 * c;
+        const bool rot = neox != 2;                  // 2: no RoPE (attention.c:129-133), bias and append only
+        const float w0 = rot ? v0 * c - v1 * s : v0, w1 = rot ? v0 * s + v1 * c : v1;
         if (i < n_head * half) {
             row[e0] = w0;
             row[e1] = w1;

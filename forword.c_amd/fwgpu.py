@@ -31,7 +31,7 @@ GGML_F32, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 2, 6, 8, 12
 BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q5_0: 22, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
 BLOCK_VALUES = {GGML_Q4_0: 32, GGML_Q5_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q6_K: 256}
 # Architectures the synthetic writer emits, as FORWORD_ARCH_* values (model_config.h:12-24).
-SYNTH_ARCHS = {"llama": 2, "qwen2": 3, "gemma": 5, "phi2": 6}
+SYNTH_ARCHS = {"gpt2": 1, "llama": 2, "qwen2": 3, "gemma": 5, "phi2": 6}
 TYPE_NAMES = {GGML_F32: "F32", GGML_Q4_0: "Q4_0", GGML_Q5_0: "Q5_0", GGML_Q8_0: "Q8_0", GGML_Q4_K: "Q4_K",
               GGML_Q6_K: "Q6_K"}
 

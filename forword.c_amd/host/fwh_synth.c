@@ -385,7 +385,7 @@ static int token_text(uint32_t i, char *buf) { return sprintf(buf, "<t%u>", i); 
 static const char *synth_arch_name(uint32_t arch)
 {
     return arch == FORWORD_ARCH_QWEN2 ? "qwen2" : arch == FORWORD_ARCH_GEMMA ? "gemma"
-         : arch == FORWORD_ARCH_PHI2 ? "phi2" : "llama";
+         : arch == FORWORD_ARCH_PHI2 ? "phi2" : arch == FORWORD_ARCH_GPT2 ? "gpt2" : "llama";
 }
 
 static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
@@ -401,32 +401,42 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         return -1;
     uint64_t hd = s->n_embd / s->n_head, kvd = hd * s->n_head_kv;
     const int phi2 = s->arch == FORWORD_ARCH_PHI2;
-    L->t = (tdesc_t *)calloc(12 * (size_t)s->n_layer + 6, sizeof(tdesc_t));
+    const int gpt2 = s->arch == FORWORD_ARCH_GPT2, ln = phi2 || gpt2;   /* LayerNorm blocks: norm biases */
+    if (gpt2 && s->n_head_kv != s->n_head) return -1;                   /* model_config.c:204 */
+    L->t = (tdesc_t *)calloc(14 * (size_t)s->n_layer + 8, sizeof(tdesc_t));
     if (!L->t) return -1;
     char nm[64];
+#define BIAS(fmt, n) do { snprintf(nm, sizeof nm, fmt, l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, n, 1, 1); } while (0)
     add_t(L, "token_embd.weight", T_EMBD, s->embd_type, s->n_embd, s->n_vocab, 2);
+    if (gpt2) add_t(L, "position_embd.weight", T_EMBD, s->embd_type, s->n_embd, s->n_ctx, 2);
     for (uint32_t l = 0; l < s->n_layer; l++) {
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l); add_t(L, nm, T_ATTN_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
-        if (phi2) { snprintf(nm, sizeof nm, "blk.%u.attn_norm.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1); }
-        snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, s->n_embd, 2);
-        snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); add_t(L, nm, T_K, s->linear_type, s->n_embd, kvd, 2);
-        snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, s->linear_type, s->n_embd, kvd, 2);
+        if (ln) BIAS("blk.%u.attn_norm.bias", s->n_embd);
+        if (gpt2) {                                   /* one [q | k | v] projection (attention.c:68-96) */
+            snprintf(nm, sizeof nm, "blk.%u.attn_qkv.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, 3 * (uint64_t)s->n_embd, 2);
+            BIAS("blk.%u.attn_qkv.bias", 3 * (uint64_t)s->n_embd);
+        } else {
+            snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, s->n_embd, 2);
+            snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); add_t(L, nm, T_K, s->linear_type, s->n_embd, kvd, 2);
+            snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, s->linear_type, s->n_embd, kvd, 2);
+        }
         if (s->arch == FORWORD_ARCH_QWEN2) {
-            snprintf(nm, sizeof nm, "blk.%u.attn_q.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1);
-            snprintf(nm, sizeof nm, "blk.%u.attn_k.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
-            snprintf(nm, sizeof nm, "blk.%u.attn_v.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, kvd, 1, 1);
+            BIAS("blk.%u.attn_q.bias", s->n_embd); BIAS("blk.%u.attn_k.bias", kvd); BIAS("blk.%u.attn_v.bias", kvd);
         }
         snprintf(nm, sizeof nm, "blk.%u.attn_output.weight", l); add_t(L, nm, T_O, s->linear_type, s->n_embd, s->n_embd, 2);
-        if (phi2) { snprintf(nm, sizeof nm, "blk.%u.attn_output.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1); }
+        if (ln) BIAS("blk.%u.attn_output.bias", s->n_embd);
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l); add_t(L, nm, T_FFN_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
-        if (phi2) { snprintf(nm, sizeof nm, "blk.%u.ffn_norm.bias", l); add_t(L, nm, T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1); }
-        if (!phi2) { snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); add_t(L, nm, T_GATE, s->linear_type, s->n_embd, s->n_ff, 2); }
+        if (ln) BIAS("blk.%u.ffn_norm.bias", s->n_embd);
+        if (!ln) { snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); add_t(L, nm, T_GATE, s->linear_type, s->n_embd, s->n_ff, 2); }
         snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l); add_t(L, nm, T_UP, s->linear_type, s->n_embd, s->n_ff, 2);
+        if (gpt2) BIAS("blk.%u.ffn_up.bias", s->n_ff);
         snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); add_t(L, nm, T_DOWN, s->linear_type, s->n_ff, s->n_embd, 2);
+        if (gpt2) BIAS("blk.%u.ffn_down.bias", s->n_embd);
     }
+#undef BIAS
     add_t(L, "output_norm.weight", T_OUT_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
-    if (phi2) add_t(L, "output_norm.bias", T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1);
-    if (s->arch != FORWORD_ARCH_GEMMA)
+    if (ln) add_t(L, "output_norm.bias", T_BIAS, FORWORD_GGML_F32, s->n_embd, 1, 1);
+    if (s->arch != FORWORD_ARCH_GEMMA && !gpt2)
         add_t(L, "output.weight", T_OUT, s->output_type, s->n_embd, s->n_vocab, 2);
 
     /* metadata: 8 <arch> keys + architecture + name + tokenizer model + tokens */

@@ -85,11 +85,12 @@ typedef struct forword_gpu forword_gpu_t;
  * max_ctx*(head_dim/2) floats (rope.c:6-17, transformer.c:73-89).
  * `max_ctx` is the already-resolved KV length (transformer.c:43-52).
  * Replaces the device-side half of transformer_init (transformer.c:14-128).
- * Every block `model_config.c:148-217` describes runs except GPT-2's (no RoPE,
- * fused attn_qkv, learned positions), which returns -1: RMSNorm or LayerNorm
+ * Every block `model_config.c:148-217` describes runs: RMSNorm or LayerNorm
  * (with biases), sequential or parallel residual, gated or plain FFN with
- * silu / gelu / gelu-tanh / relu, pairwise or NEOX RoPE, q/k/v and
- * output-projection biases, an embedding scale, a head tied to token_embd.
+ * silu / gelu / gelu-tanh / relu (GPT-2's with biases), pairwise, NEOX or no
+ * RoPE, q/k/v (separate or GPT-2's fused attn_qkv) and output-projection
+ * biases, GPT-2's learned position rows, an embedding scale, a head tied to
+ * token_embd.  Unknown norm or RoPE codes return -1.
  * head_dim 32/48/64/80/96/128/256 with any GQA group; n_embd and n_ff
  * multiples of the weight block (32 or 256 values).
  */

@@ -100,7 +100,9 @@ typedef struct {
                                      blk.N.attn_{q,k,v}.bias ~ N(0, 4*w_std); GEMMA writes
                                      no output.weight (the head reuses token_embd); PHI2
                                      writes no ffn_gate and adds F32 biases to the norms
-                                     (attn, ffn, output) and to attn_output */
+                                     (attn, ffn, output) and to attn_output; GPT2 as phi2
+                                     plus position_embd, one attn_qkv (+bias), ffn_up/down
+                                     biases and no output.weight (n_head_kv must equal n_head) */
 } fwh_synth_spec_t;
 
 /* Exact byte size of the GGUF image fwh_synth_write would produce. */

@@ -476,10 +476,13 @@ struct fwc_model {
     size_t data_size;
     lin_t embd, out_w;
     const float *out_norm, *out_norm_b;
+    lin_t pos_embd;                        /* GPT-2 learned positions */
+    float *qkv_buf;
     struct layer {
         const float *attn_norm, *ffn_norm, *attn_norm_b, *ffn_norm_b;
         const float *bq, *bk, *bv, *bo;    /* F32 biases, null when absent */
-        lin_t q, k, v, o, gate, up, down;
+        const float *bqkv, *bu, *bd;       /* GPT-2: attn_qkv.bias, ffn_up.bias, ffn_down.bias */
+        lin_t q, k, v, o, gate, up, down, qkv;
     } *L;
     const float *cos_tab, *sin_tab;
     float *kv_k, *kv_v;
@@ -516,7 +519,7 @@ void fwc_model_free(fwc_model_t *m)
     if (!m) return;
     free(m->L); free(m->kv_k); free(m->kv_v); free(m->x); free(m->xn); free(m->attn_out);
     free(m->ffn_out); free(m->q); free(m->k); free(m->v); free(m->att); free(m->gate); free(m->upb);
-    free(m->scores); free(m->logits); free(m->trace);
+    free(m->scores); free(m->logits); free(m->trace); free(m->qkv_buf);
     free(m);
 }
 
@@ -527,7 +530,7 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
     if (!data || !t || !cfg || !max_ctx || !cos_tab || !sin_tab) return NULL;
     const forword_gpu_config_t *c = cfg;
     if ((c->norm_type != FORWORD_NORM_RMS && c->norm_type != FORWORD_NORM_LAYER) ||
-        c->arch == FORWORD_ARCH_GPT2 || c->rope_type == FORWORD_ROPE_NONE || !c->n_head_kv ||
+        (c->rope_type == FORWORD_ROPE_NONE) != (c->arch == FORWORD_ARCH_GPT2) || !c->n_head_kv ||
         c->n_head % c->n_head_kv || c->head_dim % 2 || c->n_embd != c->n_head * c->head_dim) {
         fprintf(stderr, "fwc_model_init: unsupported model variant\n");
         return NULL;
@@ -547,6 +550,8 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
     if (bind_lin(&m->embd, m, e) || bind_lin(&m->out_w, m, o)) goto fail;
     m->out_norm = bind_vec(m, find(t, nt, "output_norm.weight"), c->n_embd);
     m->out_norm_b = bind_vec(m, find(t, nt, "output_norm.bias"), c->n_embd);
+    const int gpt2 = c->arch == FORWORD_ARCH_GPT2;
+    if (gpt2 && bind_lin(&m->pos_embd, m, find(t, nt, "position_embd.weight"))) goto fail;   /* transformer.c:188-205 */
     m->L = calloc(c->n_layer, sizeof(*m->L));
     if (!m->L) goto fail;
     for (uint32_t l = 0; l < c->n_layer; l++) {
@@ -554,7 +559,13 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
         struct layer *L = &m->L[l];
 #define LIN(field, suffix) snprintf(nm, sizeof nm, "blk.%u." suffix, l); \
         if (bind_lin(&L->field, m, find(t, nt, nm))) goto fail;
-        LIN(q, "attn_q.weight"); LIN(k, "attn_k.weight"); LIN(v, "attn_v.weight");
+        if (gpt2) {                                  /* attention.c:68-96 */
+            LIN(qkv, "attn_qkv.weight");
+            snprintf(nm, sizeof nm, "blk.%u.attn_qkv.bias", l);
+            L->bqkv = bind_vec(m, find(t, nt, nm), 3 * (size_t)c->n_embd);
+        } else {
+            LIN(q, "attn_q.weight"); LIN(k, "attn_k.weight"); LIN(v, "attn_v.weight");
+        }
         LIN(o, "attn_output.weight");
         if (c->use_ffn_gate) {
             LIN(gate, "ffn_gate.weight"); LIN(up, "ffn_up.weight"); LIN(down, "ffn_down.weight");
@@ -565,9 +576,16 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
             if (!tu) tu = find(t, nt, nm);
             snprintf(nm, sizeof nm, "blk.%u.fc2.weight", l);
             const forword_gpu_tensor_t *td = find(t, nt, nm);
+            const int fc2 = td != NULL;
             snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l);
             if (!td) td = find(t, nt, nm);
             if (bind_lin(&L->up, m, tu) || bind_lin(&L->down, m, td)) goto fail;
+            if (gpt2) {                              /* ffn.c:127-140: required for GPT-2 */
+                snprintf(nm, sizeof nm, "blk.%u.ffn_up.bias", l); L->bu = bind_vec(m, find(t, nt, nm), c->n_ff);
+                snprintf(nm, sizeof nm, "blk.%u.ffn_down.bias", l); L->bd = bind_vec(m, find(t, nt, nm), c->n_embd);
+                if (!L->bu || !L->bd) goto fail;
+                if (fc2) L->bd = NULL;                                   /* ffn.c:162-166 */
+            }
         }
 #undef LIN
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.bias", l);       /* transformer.c:212-230 */
@@ -596,6 +614,8 @@ fwc_model_t *fwc_model_init(const void *data, size_t data_size, const forword_gp
     m->v = calloc(kvd, 4); m->att = calloc(c->n_embd, 4); m->gate = calloc(c->n_ff, 4);
     m->upb = calloc(c->n_ff, 4); m->scores = calloc((size_t)c->n_head * max_ctx, 4);
     m->logits = calloc(c->n_vocab, 4); m->trace = calloc((size_t)2 * c->n_layer * c->n_embd, 4);
+    m->qkv_buf = calloc(3 * (size_t)c->n_embd, 4);
+    if (!m->qkv_buf) goto fail;
     if (!m->kv_k || !m->kv_v || !m->x || !m->xn || !m->attn_out || !m->ffn_out || !m->q || !m->k ||
         !m->v || !m->att || !m->gate || !m->upb || !m->scores || !m->logits || !m->trace) goto fail;
     return m;
@@ -649,11 +669,14 @@ static int ffn(fwc_model_t *m, const struct layer *L)
         return lin(&L->down, m->gate, m->ffn_out);
     }
     if (lin(&L->up, m->xn, m->upb)) return -1;
+    add_bias(m->upb, L->bu, nf);
     if (c->act_type == FORWORD_ACT_GELU_FAST) fwc_gelu_fast(m->upb, nf);
     else if (c->act_type == FORWORD_ACT_SILU) fwc_silu(m->upb, nf);
     else if (c->act_type == FORWORD_ACT_RELU) { for (size_t i = 0; i < nf; i++) if (m->upb[i] < 0.0f) m->upb[i] = 0.0f; }
     else fwc_gelu(m->upb, nf);
-    return lin(&L->down, m->upb, m->ffn_out);
+    if (lin(&L->down, m->upb, m->ffn_out)) return -1;
+    add_bias(m->ffn_out, L->bd, c->n_embd);
+    return 0;
 }
 
 float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
@@ -663,17 +686,31 @@ float *fwc_forward(fwc_model_t *m, uint32_t token, size_t pos)
     if (pos >= m->n_ctx || token >= c->n_vocab) return NULL;     /* transformer.c:156-164 */
     if (get_row(&m->embd, token, m->x)) return NULL;             /* transformer.c:167-177 */
     if (c->embd_scale != 1.0f) for (size_t i = 0; i < n; i++) m->x[i] *= c->embd_scale;
+    if (c->arch == FORWORD_ARCH_GPT2) {                          /* transformer.c:188-205 */
+        if (get_row(&m->pos_embd, pos, m->xn)) return NULL;
+        for (size_t i = 0; i < n; i++) m->x[i] += m->xn[i];
+    }
     int neox = c->rope_type == FORWORD_ROPE_NEOX;
     for (uint32_t l = 0; l < c->n_layer; l++) {                  /* transformer.c:208-290 */
         struct layer *L = &m->L[l];
         block_norm(m, L->attn_norm, L->attn_norm_b);
         /* attention_forward (attention.c:97-166) */
-        if (lin(&L->q, m->xn, m->q) || lin(&L->k, m->xn, m->k) || lin(&L->v, m->xn, m->v)) return NULL;
-        add_bias(m->q, L->bq, n);                                /* linear.c:214-221 */
-        add_bias(m->k, L->bk, kvd);
-        add_bias(m->v, L->bv, kvd);
-        fwc_rope_apply(m->q, pos, c->n_head, hd, m->cos_tab, m->sin_tab, neox);
-        fwc_rope_apply(m->k, pos, c->n_head_kv, hd, m->cos_tab, m->sin_tab, neox);
+        if (c->arch == FORWORD_ARCH_GPT2) {                      /* attention.c:68-96: q | k | v */
+            if (lin(&L->qkv, m->xn, m->qkv_buf)) return NULL;
+            add_bias(m->qkv_buf, L->bqkv, 3 * n);
+            memcpy(m->q, m->qkv_buf, n * 4);
+            memcpy(m->k, m->qkv_buf + n, n * 4);
+            memcpy(m->v, m->qkv_buf + 2 * n, n * 4);
+        } else {
+            if (lin(&L->q, m->xn, m->q) || lin(&L->k, m->xn, m->k) || lin(&L->v, m->xn, m->v)) return NULL;
+            add_bias(m->q, L->bq, n);                            /* linear.c:214-221 */
+            add_bias(m->k, L->bk, kvd);
+            add_bias(m->v, L->bv, kvd);
+        }
+        if (c->rope_type != FORWORD_ROPE_NONE) {                 /* attention.c:129-133 */
+            fwc_rope_apply(m->q, pos, c->n_head, hd, m->cos_tab, m->sin_tab, neox);
+            fwc_rope_apply(m->k, pos, c->n_head_kv, hd, m->cos_tab, m->sin_tab, neox);
+        }
         memcpy(fwc_kv_k(m, l, pos), m->k, kvd * 4);
         memcpy(fwc_kv_v(m, l, pos), m->v, kvd * 4);
         fwc_attention_core(m->q, fwc_kv_k(m, l, 0), fwc_kv_v(m, l, 0), m->att, c->n_head,

@@ -102,6 +102,10 @@ static float *traced_forward(transformer_t *t, uint32_t tok, size_t pos, float *
     if (linear_get_row(g, tensor_find(g, "token_embd.weight"), tok, t->x)) return NULL;
     if (c->embd_scale != 1.0f)                                      /* transformer.c:179-182 */
         for (size_t i = 0; i < n; i++) t->x[i] *= c->embd_scale;
+    if (c->arch == ARCH_GPT2) {                                     /* transformer.c:188-205 */
+        if (linear_get_row(g, tensor_find(g, "position_embd.weight"), pos, t->xn)) return NULL;
+        for (size_t i = 0; i < n; i++) t->x[i] += t->xn[i];
+    }
     for (size_t l = 0; l < c->n_layer; l++) {
         const float *an = vec(g, "blk.%zu.attn_norm.weight", l), *anb = vec(g, "blk.%zu.attn_norm.bias", l);
         const float *fn = vec(g, "blk.%zu.ffn_norm.weight", l), *fnb = vec(g, "blk.%zu.ffn_norm.bias", l);

@@ -22,7 +22,9 @@ Q4K, Q6K = fwgpu.GGML_Q4_K, fwgpu.GGML_Q6_K
 # config loader), 8/2 heads, Q8_0 linears.  "gemma": gated FFN with the tanh
 # GELU, embedding rows times sqrt(n_embd), lm-head tied to token_embd.
 # "phi2": LayerNorm with biases, parallel residual, plain GELU-tanh FFN,
-# NEOX RoPE, attn_output bias; 4 heads of 64.
+# NEOX RoPE, attn_output bias; 4 heads of 64.  "gpt2": LayerNorm, fused
+# attn_qkv with bias, learned position embeddings, no RoPE, plain erf-GELU FFN
+# with biases, lm-head tied to token_embd.
 MODELS = {
     "tiny": {"spec": lambda: fwgpu.spec_tiny(seed=20240601), "n_prompt": 16, "n_gen": 128,
              "max_ctx": 0, "prompt_seed": 1},
@@ -38,6 +40,8 @@ MODELS = {
               "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 5},
     "phi2": {"spec": lambda: fwgpu.spec(256, 1024, 2, 4, 4, 1000, 64, 10000.0, seed=321, arch="phi2"),
              "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 6},
+    "gpt2": {"spec": lambda: fwgpu.spec(256, 1024, 2, 4, 4, 1000, 64, 10000.0, seed=654, arch="gpt2"),
+             "n_prompt": 8, "n_gen": 24, "max_ctx": 0, "prompt_seed": 7},
 }
 
 

@@ -59,19 +59,17 @@ def test_model_calls_reject_null_handle():
 
 
 def test_init_rejects_unsupported_variant():
-    """A GPT-2 style config (no RoPE: learned positions, fused QKV) is refused with -1, not run."""
+    """An unknown norm type is refused with -1, not run."""
     sp = fwgpu.spec(256, 512, 2, 8, 2, 1000, 64)
     with fwgpu.HostModel(synth=sp) as host:
         cfg = fwgpu.Config.from_buffer_copy(host.cfg)
-        cfg.norm_type = 1
-        cfg.use_ffn_gate = 0
-        cfg.rope_type = 2
+        cfg.norm_type = 5
         h = C.c_void_p()
         rc = fwgpu.gpu_lib().forword_gpu_init(C.byref(h), host.data, host.data_size, host.tensors,
                                               host.n_tensors, C.byref(cfg), host.n_ctx,
                                               host.cos.ctypes.data_as(fwgpu.fp), host.sin.ctypes.data_as(fwgpu.fp))
         assert rc == -1 and not h.value
-        assert "GPT-2 style" in fwgpu.last_error()
+        assert "unknown norm or RoPE type" in fwgpu.last_error()
 
 
 def test_operator_argument_checks_match_reference():

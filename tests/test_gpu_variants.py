@@ -285,3 +285,34 @@ def test_head_dims_and_groups_match_oracle(name):
             ref = om.forward(int(t), pos)
         close(lg, ref, f"{name} prefill logits")
         assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+
+
+def test_gpt2_matches_oracle():
+    """GPT-2 block (model_config.c:197-207): learned position rows added to the
+    embedding (transformer.c:188-205), one [q | k | v] projection with its bias
+    (attention.c:68-96), no RoPE, LayerNorm, plain erf-GELU FFN with up/down
+    biases (ffn.c:127-168), head tied to token_embd: decode, prefill, greedy."""
+    fw_cpu.set_threads(8)
+    sp = fwgpu.spec(512, 2048, 2, 8, 8, 2048, 96, 10000.0, linear_type=Q4, seed=61, arch="gpt2")
+    with fwgpu.HostModel(synth=sp) as host, fwgpu.GpuModel(host) as gm, fw_cpu.OracleModel(host) as om:
+        c = host.cfg
+        assert (c.arch, c.rope_type, c.norm_type, c.use_ffn_gate, c.act_type) == (1, 2, 1, 0, 1)
+        assert not gm.persistent
+        toks = np.random.default_rng(16).integers(3, c.n_vocab, 10)
+        for pos, t in enumerate(toks):
+            lg, ref = gm.forward(int(t), pos), om.forward(int(t), pos)
+            close(lg, ref, f"logits at position {pos}")
+            assert fw_cpu.argmax(lg) == fw_cpu.argmax(ref)
+            if pos in (0, 9):
+                close(gm.layer_trace().reshape(-1), om.trace().reshape(-1), f"residual stream at {pos}")
+        got = gm.generate_greedy(toks[:4].astype(np.uint32), 12)
+        assert np.array_equal(got, om.generate_greedy(toks[:4].astype(np.uint32), 12))
+        prompt = np.random.default_rng(17).integers(3, c.n_vocab, 40).astype(np.uint32)
+        lg = gm.prefill(prompt)
+        for pos, t in enumerate(prompt):
+            ref = om.forward(int(t), pos)
+        close(lg, ref, "prefill logits")
+        k, v = gm.kv_read(1, 0, len(prompt))
+        kr, vr = om.kv(1, 39)
+        close(k[39], kr, "prefill K row (no RoPE)")
+        close(v[39], vr, "prefill V row")
