@@ -196,7 +196,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "qwen2-7b", "phi2", "tiny"])
+    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "qwen2-7b", "phi2", "gpt2-xl", "tiny"])
     ap.add_argument("--mode", default="full", choices=["full", "decode", "copy"])
     ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -229,6 +229,9 @@ def main():
     elif args.config == "qwen2-7b":
         sp = fwgpu.spec_qwen2_7b(n_ctx=max(768, n_ctx))
         workload = "Qwen2-7B-shape Q4_0 greedy decode (q/k/v biases, GQA group 7; Q8_0 embedding/output)"
+    elif args.config == "gpt2-xl":
+        sp = fwgpu.spec_gpt2_xl(n_ctx=max(768, n_ctx))
+        workload = "GPT-2-XL-shape Q8_0 greedy decode (learned positions, fused QKV, LayerNorm, no RoPE)"
     elif args.config == "phi2":
         sp = fwgpu.spec_phi2(n_ctx=max(768, n_ctx))
         workload = "Phi-2-shape Q4_0 greedy decode (LayerNorm, parallel residual, NEOX RoPE, hd 80)"
@@ -283,7 +286,8 @@ def main():
 
     total_ms, launches = timed_decode(hip, gm, args.steps)
     tok_s = args.steps / (total_ms / 1e3)
-    bb = {"8b-k": dict(linear_bb=18, embd_bb=18, out_bb=26.25)}.get(args.config, {})   # per 32 values
+    bb = {"8b-k": dict(linear_bb=18, embd_bb=18, out_bb=26.25),                      # per 32 values
+          "gpt2-xl": dict(linear_bb=34)}.get(args.config, {})
     byte_list = [step_bytes(cfg, p, **bb) for p in range(p0, p0 + args.steps)]
     avg_bytes = float(np.mean(byte_list))
     log(f"decode: {args.steps} steps at positions {p0}..{p0 + args.steps - 1} in {total_ms:.2f} ms "

@@ -109,6 +109,13 @@ def spec_phi2(seed=22, n_ctx=768, **kw):
     return spec(2560, 10240, 32, 32, 32, 51200, n_ctx, 10000.0, seed=seed, arch="phi2", **kw)
 
 
+def spec_gpt2_xl(seed=48, n_ctx=768, **kw):
+    """GPT-2 XL shape: dim 1600, 48 layers, 25 heads (hd 64), ffn 6400, vocab 50257, learned
+    positions, fused attn_qkv, LayerNorm, erf-GELU FFN with biases; Q8_0 linears."""
+    kw.setdefault("linear_type", GGML_Q8_0)
+    return spec(1600, 6400, 48, 25, 25, 50257, n_ctx, 10000.0, seed=seed, arch="gpt2", **kw)
+
+
 _host = None
 _gpu = None
 
