@@ -62,6 +62,7 @@ struct QmvArgs {
     float *scale_out;
     float norm_eps;
     uint32_t act;              // SWIGLU: FfnAct of the gate (silu / gelu / gelu-tanh)
+    uint32_t store_act;        // STORE: 0, or 1 + FfnAct applied after the bias (plain FFN up, ffn.c:143-160)
 };
 
 // Rows computed by one wave of the GEMV kernels.

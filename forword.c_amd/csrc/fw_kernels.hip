@@ -310,7 +310,11 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
         if (lane == 0)
 #pragma unroll
             for (int k = 0; k < R; k++)
-                if (ok[k]) a.out[seg][row[k]] = a.bias[seg] ? acc[k] + a.bias[seg][row[k]] : acc[k];
+                if (ok[k]) {
+                    float v = a.bias[seg] ? acc[k] + a.bias[seg][row[k]] : acc[k];
+                    if (a.store_act) v = ffn_act(v, a.store_act - 1);
+                    a.out[seg][row[k]] = v;
+                }
     } else if constexpr (EPI == EPI_RESID) {
         float ss = 0.f;
         if (lane == 0)

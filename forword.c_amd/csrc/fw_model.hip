@@ -312,9 +312,9 @@ static hipError_t enqueue_step_generic(forword_gpu_t *h)
             QmvArgs a{};
             a.n_seg = 1; a.w[0] = Ly.up.w; a.rows[0] = c.n_ff; a.n_cols = n; a.row_bytes = Ly.up.row_bytes;
             a.x = h->d_xn; a.out[0] = h->d_h; a.bias[0] = Ly.bu;
+            a.store_act = 1 + plain_act_code(c);                                       // act(W x + b) in the epilogue
             qmv_plan(a, EPI_STORE);
             TRY(launch_qmv(Ly.up.type, EPI_STORE, a, s));
-            TRY(launch_act(h->d_h, h->d_h, c.n_ff, plain_act_code(c), s));
         }
         {
             QmvArgs a{};                                                                // ffn.c:106/168, transformer.c:250/287
