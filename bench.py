@@ -205,7 +205,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this decode path runs on one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(the path is built for one GPU; sharding across GPUs is a design, not code)", file=sys.stderr)
         sys.exit(2)
     hip = Hip()
     if args.mode == "copy":
