@@ -125,3 +125,27 @@ def test_qwen2_synth_config():
             for r, n in (("q", 256), ("k", 64), ("v", 64)):
                 t = names[f"blk.{l}.attn_{r}.bias"]
                 assert t.ggml_type == 0 and t.n_dims == 1 and t.dims[0] == n
+
+
+
+@pytest.mark.parametrize("arch,expect", [
+    # (arch, norm, act, gate, rope, qkv_bias, parallel, embd_scale) as model_config.c:148-217 sets them
+    ("llama", (2, 0, 0, 1, 0, 0, 0, 1.0)),
+    ("gemma", (5, 0, 2, 1, 0, 0, 0, 16.0)),
+    ("phi2", (6, 1, 2, 0, 1, 0, 1, 1.0)),
+    ("gpt2", (1, 1, 1, 0, 2, 1, 0, 1.0)),
+])
+def test_synth_arch_config(arch, expect):
+    """Each synthetic architecture reads back with the reference's per-architecture
+    block settings (the config reader mirrors model_config.c)."""
+    sp = fwgpu.spec(256, 512, 1, 4, 4, 300, 32, 10000.0, arch=arch)
+    with fwgpu.HostModel(synth=sp) as host:
+        c = host.cfg
+        got = (c.arch, c.norm_type, c.act_type, c.use_ffn_gate, c.rope_type, c.use_qkv_bias, c.parallel_res,
+               round(c.embd_scale, 4))
+        assert got == expect
+        names = {host.tensors[i].name.decode() for i in range(host.n_tensors)}
+        assert ("output.weight" in names) == (arch in ("llama", "phi2"))        # gemma, gpt2: tied head
+        assert ("blk.0.attn_qkv.weight" in names) == (arch == "gpt2")
+        assert ("position_embd.weight" in names) == (arch == "gpt2")
+        assert ("blk.0.ffn_gate.weight" in names) == (arch in ("llama", "gemma"))

@@ -15,7 +15,7 @@ SETTINGS = [(0.0, 0.9, 1.3, 1), (0.8, 0.9, 1.1, 12345), (1.0, 0.95, 1.0, 77), (1
             (0.6, 0.3, 1.05, 0)]
 
 
-@pytest.mark.parametrize("name", ["gqa", "q5"])
+@pytest.mark.parametrize("name", ["gqa", "q5", "qwen2", "phi2", "gpt2"])   # persistent and per-phase steps
 def test_sampled_generation_matches_oracle(name):
     m = gs.MODELS[name]
     prompt = gs.prompt(name)
