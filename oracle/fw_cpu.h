@@ -21,8 +21,10 @@
  *   fwc_rms_norm        test_runner.c:30-41 invariant, reference rms_norm bit-exact
  *   fwc_rope_apply      test_runner.c:60-90 (pos 0 identity), reference bit-exact
  *   fwc_softmax/attention/ffn/forward  reference transformer_forward bit-exact
- *                       (golden fixtures of the llama, qwen2, gemma and phi2
- *                       blocks), per-layer residual stream
+ *                       (golden fixtures of the llama, qwen2, gemma, phi2 and
+ *                       gpt2 blocks), per-layer residual stream; the gpt2
+ *                       fixture pins learned positions, the fused attn_qkv and
+ *                       the FFN biases
  *   fwc_layer_norm      the phi2 fixture (bit-exact through the whole forward)
  *   fwc_gelu_fast       the gemma and phi2 fixtures; float64 closed form
  *   fwc_gelu            float64 closed form only (no fixture selects it)
