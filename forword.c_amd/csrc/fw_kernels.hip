@@ -270,16 +270,49 @@ __global__ __launch_bounds__(256) void k_qmv(QmvArgs a)
                         s = __builtin_fmaf(ds * (float)v - dm, xv[i], s);
                     }
                 } else {
+                    // Q6_K (quant.c:160-183): 32 code bytes of ql (low or high nibbles) and
+                    // 32 of qh (2 bits each) as dwords from the 2-byte-aligned block, four
+                    // 6-bit codes per dword; per 16 values (d·sc)·(Σq·x − 32·Σx).
                     const uint32_t h = g / 4, kk = g % 4;
-                    const uint8_t *ql = blk + h * 64 + 32 * (kk & 1), *qh = blk + 128 + h * 32;
                     const float d = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
                     const float s0 = d * (float)(int8_t)blk[192 + h * 8 + 2 * kk];
                     const float s1 = d * (float)(int8_t)blk[192 + h * 8 + 2 * kk + 1];
+                    auto load8 = [](const uint8_t *p, uint32_t (&o)[8]) {      // 32 bytes at a 2-byte-aligned p
+                        const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
+                        const uint32_t *w = reinterpret_cast<const uint32_t *>(ad & ~(uintptr_t)3);
+                        uint32_t t[9];
 #pragma unroll
-                    for (int l = 0; l < 32; l++) {
-                        const int q = (int)(((kk >= 2) ? (ql[l] >> 4) : (ql[l] & 15)) | (((qh[l] >> (2 * kk)) & 3) << 4));
-                        s = __builtin_fmaf((l < 16 ? s0 : s1) * (float)(q - 32), xv[l], s);
+                        for (int i = 0; i < 9; i++) t[i] = w[i];             // inside the 210-byte block
+#pragma unroll
+                        for (int i = 0; i < 8; i++) o[i] = (ad & 2) ? align16(t[i + 1], t[i]) : t[i];
+                    };
+                    if (reinterpret_cast<uintptr_t>(blk) & 1) {               // odd address: byte loads
+                        const uint8_t *ql = blk + h * 64 + 32 * (kk & 1), *qh = blk + 128 + h * 32;
+#pragma unroll
+                        for (int l = 0; l < 32; l++) {
+                            const int q = (int)(((kk >= 2) ? (ql[l] >> 4) : (ql[l] & 15)) |
+                                                (((qh[l] >> (2 * kk)) & 3) << 4));
+                            s = __builtin_fmaf((l < 16 ? s0 : s1) * (float)(q - 32), xv[l], s);
+                        }
+                        acc[k] += s;
+                        continue;
                     }
+                    uint32_t lw[8], hw[8];
+                    load8(blk + h * 64 + 32 * (kk & 1), lw);
+                    load8(blk + 128 + h * 32, hw);
+                    float a0 = 0.f, a1 = 0.f, x0 = 0.f, x1 = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const uint32_t nib = (kk >= 2 ? lw[i] >> 4 : lw[i]) & 0x0F0F0F0Fu;
+                        const uint32_t q4 = nib | (((hw[i] >> (2 * kk)) & 0x03030303u) << 4);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float q = (float)((q4 >> (8 * e)) & 0xFFu), xx = xv[4 * i + e];
+                            if (i < 4) { a0 = __builtin_fmaf(q, xx, a0); x0 += xx; }
+                            else { a1 = __builtin_fmaf(q, xx, a1); x1 += xx; }
+                        }
+                    }
+                    s = s0 * __builtin_fmaf(-32.0f, x0, a0) + s1 * __builtin_fmaf(-32.0f, x1, a1);
                 }
                 acc[k] += s;
             }
