@@ -129,7 +129,9 @@ def timed_decode(hip, gm, steps):
 
 
 def microbench(hip, min_bytes=1 << 30, reps=48):
-    """quant_matvec (operator entry point) GB/s at the microbenchmark shapes."""
+    """quant_matvec (operator entry point) GB/s at the microbenchmark shapes: `reps`
+    back-to-back calls over rotating weight copies (>= 1 GiB, so the 256 MB
+    last-level cache cannot serve repeats), one event pair around all of them."""
     L = fwgpu.gpu_lib()
     out = []
     x = fwgpu.DeviceBuffer.from_array(fwgpu.randn(7, 14336))
@@ -143,41 +145,89 @@ def microbench(hip, min_bytes=1 << 30, reps=48):
             for i in range(copies):                                 # warm-up pass
                 assert L.forword_gpu_quant_matvec(bufs[i].ptr, w.nbytes, t, x.ptr, y.ptr, cols, rows, None) == 0
             hip.sync(None)
-            ev = [hip.event() for _ in range(reps + 1)]
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0, None)
             for i in range(reps):
-                hip.record(ev[i], None)
                 assert L.forword_gpu_quant_matvec(bufs[i % copies].ptr, w.nbytes, t, x.ptr, y.ptr,
                                                   cols, rows, None) == 0
-            hip.record(ev[reps], None)
+            hip.record(e1, None)
             hip.sync(None)
-            us = float(np.mean([hip.ms(ev[i], ev[i + 1]) for i in range(reps)])) * 1e3
+            us = hip.ms(e0, e1) * 1e3 / reps
             for b in bufs:
                 b.free()
             gbs = algo / (us * 1e-6) / 1e9
             out.append({"type": fwgpu.TYPE_NAMES[t], "rows": rows, "cols": cols, "bytes": algo,
-                        "us": round(us, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
-            log(f"microbench {fwgpu.TYPE_NAMES[t]} {rows}x{cols}: {us:.2f} us, {gbs:.0f} GB/s")
+                        "us_per_call": round(us, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"microbench {fwgpu.TYPE_NAMES[t]} {rows}x{cols}: {us:.2f} us per call, {gbs:.0f} GB/s")
     x.free()
     y.free()
     return out
 
 
-def cpu_baseline(host, budget_s):
-    """The oracle (same fp32 arithmetic as forword.c, Q4_0 added) on one core."""
+def host_cpu():
+    """CPU model name and the number of cores this process may use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(host, budget_s, p0):
+    """The oracle (same fp32 arithmetic as forword.c, Q4_0 added) on one pinned core,
+    timed at the decode positions p0, p0+1, ...: KV rows 0..p0-1 are filled first
+    (N(0,1)), so every timed forward attends over as many rows as a decode step."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import fw_cpu
-    fw_cpu.set_threads(1)
-    om = fw_cpu.OracleModel(host)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        om.forward(3 + done, done)
-        done += 1
-        el = time.perf_counter() - t0
-        log(f"cpu baseline: {done} forwards in {el:.1f}s")
-        if el + el / done > budget_s or done >= 64:
-            break
-    om.close()
-    return done / el, done, el
+    model, ncpu = host_cpu()
+    keep = os.sched_getaffinity(0)
+    core = min(keep)
+    os.sched_setaffinity(0, {core})
+    try:
+        fw_cpu.set_threads(1)
+        om = fw_cpu.OracleModel(host)
+        c = host.cfg
+        kvd = c.n_head_kv * c.head_dim
+        rng = np.random.default_rng(11)
+        k = rng.standard_normal((p0, kvd), dtype=np.float32)
+        v = rng.standard_normal((p0, kvd), dtype=np.float32)
+        for layer in range(c.n_layer):
+            om.set_kv(layer, 0, k, v)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            om.forward(3 + done, p0 + done)
+            done += 1
+            el = time.perf_counter() - t0
+            log(f"cpu baseline: {done} forwards at positions {p0}.. in {el:.1f}s")
+            if el + el / done > budget_s or done >= 64:
+                break
+        om.close()
+    finally:
+        os.sched_setaffinity(0, keep)
+    return done / el, done, el, model, ncpu, core
+
+
+def copy_gbs(hip, mb=1024, reps=8):
+    """Device-to-device copy rate (bytes read + written per second) of an mb MiB
+    buffer: the practical ceiling of a pure streaming kernel on this GPU."""
+    n = mb << 20
+    a, b = fwgpu.DeviceBuffer(n), fwgpu.DeviceBuffer(n)
+    assert hip.L.hipMemcpyAsync(b.ptr, a.ptr, n, 3, None) == 0
+    hip.sync(None)
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0, None)
+    for _ in range(reps):
+        assert hip.L.hipMemcpyAsync(b.ptr, a.ptr, n, 3, None) == 0
+    hip.record(e1, None)
+    hip.sync(None)
+    ms = hip.ms(e0, e1)
+    a.free()
+    b.free()
+    return 2.0 * n * reps / (ms / 1e3) / 1e9
 
 
 def copy_calibration(hip, mb):
@@ -285,6 +335,7 @@ def main():
     hip.sync(gm.stream)
 
     total_ms, launches = timed_decode(hip, gm, args.steps)
+    gm.status()                     # raises if a launch gave up at a bounded wait: no number from it
     tok_s = args.steps / (total_ms / 1e3)
     bb = {"8b-k": dict(linear_bb=18, embd_bb=18, out_bb=26.25),                      # per 32 values
           "gpt2-xl": dict(linear_bb=34)}.get(args.config, {})
@@ -293,6 +344,8 @@ def main():
     log(f"decode: {args.steps} steps at positions {p0}..{p0 + args.steps - 1} in {total_ms:.2f} ms "
         f"-> {tok_s:.1f} tok/s, {avg_bytes * tok_s / 1e9:.0f} GB/s effective")
     if args.mode == "decode":
+        gm.close()                  # handle, stream and pinned buffers released before the process exits
+        host.close()
         print(json.dumps({"tok_s": round(tok_s, 2), "steps": args.steps, "ms": round(total_ms, 3)}), flush=True)
         return
     if gm.persistent and os.environ.get("FORWORD_GPU_PHASE_TIMES") == "1":
@@ -319,13 +372,16 @@ def main():
     if not args.no_microbench and args.config == "8b":
         micro = microbench(hip)
     gm.close()
+    copy = copy_gbs(hip)
+    log(f"device-to-device copy: {copy:.0f} GB/s (read + write)")
 
     cpu = None
     if not args.no_cpu and args.config == "8b":
-        v, n, el = cpu_baseline(host, args.cpu_seconds)
+        v, n, el, model, ncpu, core = cpu_baseline(host, args.cpu_seconds, p0)
         cpu = {"value": round(v, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-               "sample": f"{n} forwards of the same model at positions 0..{n - 1}, 1 thread, "
-                         f"{el:.1f} s (oracle/fw_cpu.c: forword.c's fp32 order, Q4_0 added)"}
+               "sample": f"{n} forwards of the same model at decode positions {p0}..{p0 + n - 1} "
+                         f"(KV rows 0..{p0 - 1} filled), 1 thread pinned to core {core} of {ncpu} "
+                         f"({model}), {el:.1f} s (oracle/fw_cpu.c: forword.c's fp32 order, Q4_0 added)"}
     host.close()
 
     cfg_out = {"workload": workload, "step_impl": step_impl,
@@ -340,12 +396,15 @@ def main():
         cfg_out["prefill_batched_tok_s"] = round(args.prompt / prefill_b_s, 1)
         cfg_out["prefill_batched_same_first_token"] = bool(int(first_b) == int(first[0]))
         cfg_out["first_token"] = int(first[0])
-    traffic, traffic_src = None, None
+    traffic, traffic_src, traffic_ratio = None, None, None
     tf = os.path.join(ROOT, "profiles", "k_decode_8b_q4_0_traffic.json")
     if args.config == "8b" and gm_persistent and os.path.exists(tf):
-        # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE runs of this workload
+        # HBM bytes per step from the committed FETCH_SIZE / WRITE_SIZE runs of this
+        # workload, scaled to the steps of the launch timed here
         t = json.load(open(tf))
-        traffic, traffic_src = t["traffic_bytes_per_launch"], t["source"]
+        traffic = int(t["traffic_bytes_per_step"] * n_l)
+        traffic_ratio = round(t["traffic_bytes_per_step"] / t["algorithmic_bytes_per_step"], 4)
+        traffic_src = t["source"]
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
@@ -353,7 +412,9 @@ def main():
         "data": "synthetic (seeded random-init GGUF, random prompt ids)",
         "config": cfg_out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_vs_algorithmic": traffic_ratio, "traffic_source": traffic_src,
+                     "copy_gbs": round(copy, 1), "frac_of_copy": round(achieved / copy, 4),
                      "kernel": (f"k_decode (persistent token step, {n_l} steps per launch)" if gm_persistent
                                 else f"per-phase step kernels replayed from a hipGraph, {n_l} steps per timing"),
                      "bytes_per_launch": int(launch_bytes), "avg_ms_per_launch": round(launch_ms, 3)},

@@ -1170,6 +1170,13 @@ extern "C" size_t forword_gpu_n_ctx(const forword_gpu_t *h) { return h ? h->n_ct
 extern "C" void *forword_gpu_stream(const forword_gpu_t *h) { return h ? (void *)h->stream : nullptr; }
 extern "C" int forword_gpu_step_impl(const forword_gpu_t *h) { return h && h->mk ? 1 : 0; }
 
+extern "C" int forword_gpu_status(forword_gpu_t *h)
+{
+    if (!h) { set_err("status: NULL handle"); return -1; }
+    HIPCHK(hipStreamSynchronize(h->stream), "status");
+    return mk_check(h);
+}
+
 extern "C" int forword_gpu_phase_times(forword_gpu_t *h, double *us, size_t n)
 {
     if (!h || !us) { set_err("phase_times: invalid arguments"); return -1; }

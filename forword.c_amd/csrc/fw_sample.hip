@@ -139,7 +139,9 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ bu
         if (t == 0) {
             float acc = 0.f;
             uint32_t b = kSampBuckets, cnt = 0;
-            while (b > 0 && acc < top_p) { b--; acc += bsum[b]; cnt += bcnt[b]; }
+            // at least the highest non-empty bucket: with top_p <= 0 the nucleus
+            // is the single most probable token (sampler.c:71-76 stops at i = 0)
+            do { b--; acc += bsum[b]; cnt += bcnt[b]; } while (b > 0 && (acc < top_p || cnt == 0));
             uint32_t sel = b > 0 ? b - 1 : 0;                        // one bucket of margin
             if (cnt + (b > 0 ? bcnt[b - 1] : 0) > cap) sel = b;          // no room for the margin
             s_sel = sel;

@@ -194,6 +194,7 @@ def gpu_lib():
         _sig(L, "forword_gpu_n_ctx", sz, [vp])
         _sig(L, "forword_gpu_stream", vp, [vp])
         _sig(L, "forword_gpu_step_impl", C.c_int, [vp])
+        _sig(L, "forword_gpu_status", C.c_int, [vp])
         _sig(L, "forword_gpu_phase_times", C.c_int, [vp, C.POINTER(C.c_double), sz])
         _sig(L, "forword_gpu_last_error", C.c_char_p, [])
         _sig(L, "forword_gpu_quant_matvec", C.c_int, [vp, sz, u32, vp, vp, sz, sz, vp])
@@ -361,6 +362,10 @@ class GpuModel:
         if got < 0:
             raise ForwordError(f"phase_times failed: {last_error()}")
         return out[:got]
+
+    def status(self):
+        """Wait for the queued work; raise if a persistent launch gave up at a bounded wait."""
+        _check(gpu_lib().forword_gpu_status(self.h), "status")
 
     @property
     def persistent(self) -> bool:

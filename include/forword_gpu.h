@@ -217,6 +217,16 @@ void *forword_gpu_stream(const forword_gpu_t *h);
 int forword_gpu_step_impl(const forword_gpu_t *h);
 
 /*
+ * Wait for the work queued on the handle's stream and report whether it ran
+ * to the end: -1 when a persistent step launch gave up at a bounded wait (its
+ * results, and those of the launches queued after it, are invalid; the error
+ * state is reset so the handle can be used again), 0 otherwise.  The decode
+ * calls that only queue work (out_ids == NULL) leave this check to the caller.
+ * No counterpart in forword.c, whose step cannot fail this way.
+ */
+int forword_gpu_status(forword_gpu_t *h);
+
+/*
  * Profiling aid of the persistent step kernel (no counterpart in forword.c):
  * with FORWORD_GPU_PHASE_TIMES=1 set before forword_gpu_init, the kernel
  * stamps the wall clock after every phase.  Writes the mean duration in

@@ -55,6 +55,7 @@ def test_model_calls_reject_null_handle():
     assert L.forword_gpu_kv_write(None, 0, 0, 1, None, None) == -1
     assert L.forword_gpu_layer_trace(None, None) == -1
     assert L.forword_gpu_n_ctx(None) == 0
+    assert L.forword_gpu_status(None) == -1
     L.forword_gpu_free(None)
 
 

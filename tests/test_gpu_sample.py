@@ -12,7 +12,7 @@ import golden_specs as gs
 pytestmark = pytest.mark.gpu
 
 SETTINGS = [(0.0, 0.9, 1.3, 1), (0.8, 0.9, 1.1, 12345), (1.0, 0.95, 1.0, 77), (1.5, 0.5, 1.2, 2 ** 40 + 3),
-            (0.6, 0.3, 1.05, 0)]
+            (0.6, 0.3, 1.05, 0), (0.9, 0.0, 1.1, 31)]          # top_p 0: the nucleus is the top token
 
 
 @pytest.mark.parametrize("name", ["gqa", "q5", "qwen2", "phi2", "gpt2"])   # persistent and per-phase steps
@@ -32,6 +32,15 @@ def test_sampled_generation_greedy_equals_greedy_loop():
     prompt = gs.prompt("gqa")
     with fwgpu.HostModel(synth=m["spec"]()) as host, fwgpu.GpuModel(host) as gm:
         assert np.array_equal(gm.generate(prompt, 16, 0.0, 0.9, 1.0, 5), gm.generate_greedy(prompt, 16))
+
+
+def test_sampled_generation_repeats_bitwise():
+    # the same seed gives the same tokens: no order-dependent accumulation decides a draw
+    m = gs.MODELS["gqa"]
+    prompt = gs.prompt("gqa")
+    with fwgpu.HostModel(synth=m["spec"]()) as host, fwgpu.GpuModel(host) as gm:
+        runs = [gm.generate(prompt, 24, 1.2, 0.9, 1.1, 4242) for _ in range(3)]
+        assert all(np.array_equal(runs[0], r) for r in runs[1:])
 
 
 def test_sampled_generation_nucleus_too_large():
