@@ -99,6 +99,7 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc, fl
                             uint32_t n_head, uint32_t n_kv, uint32_t head_dim, uint32_t n_splits,
                             const StepState *st, uint32_t pos_host, hipStream_t s);
 
+hipError_t launch_set_state(StepState *st, const StepState &v, hipStream_t s);
 hipError_t launch_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *counter,
                          uint32_t *out, StepState *st, const uint32_t *prompt, uint32_t *ids,
                          uint32_t n_blocks, hipStream_t s);

@@ -942,6 +942,20 @@ static uint32_t ew_blocks(uint64_t n)
     return (uint32_t)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
 }
 
+// The step state as the host sets it, taken by value at launch: stream-ordered
+// behind the work already queued, with no host buffer the host could change
+// before a copy engine reads it.
+__global__ void k_set_state(StepState *st, StepState v)
+{
+    if (threadIdx.x == 0) *st = v;
+}
+
+hipError_t launch_set_state(StepState *st, const StepState &v, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_set_state, dim3(1), dim3(64), 0, s, st, v);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, uint64_t n, hipStream_t s)
 {
     hipLaunchKernelGGL(k_silu_mul, dim3(ew_blocks(n)), dim3(256), 0, s, g, u, out, n);

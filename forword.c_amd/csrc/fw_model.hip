@@ -136,7 +136,8 @@ struct forword_gpu {
     bool generic = false;
     float *d_ao = nullptr;                           // attention output kept for the parallel residual
     uint32_t *d_ticket = nullptr;
-    StepState *d_state = nullptr, *h_state = nullptr;
+    StepState *d_state = nullptr, *h_state = nullptr;   // h_state: the host's mirror, set on the device by kernel
+    StepState host_state{};                             // argument (launch_set_state), never copied by DMA
     float *h_logits = nullptr;
     uint32_t *h_u32 = nullptr;
     uint32_t n_splits = 1, am_blocks = 1;
@@ -602,7 +603,6 @@ extern "C" void forword_gpu_free(forword_gpu_t *h)
     if (h->exec) (void)hipGraphExecDestroy(h->exec);
     if (h->graph) (void)hipGraphDestroy(h->graph);
     for (void *p : h->allocs) (void)hipFree(p);
-    if (h->h_state) (void)hipHostFree(h->h_state);
     if (h->h_logits) (void)hipHostFree(h->h_logits);
     if (h->h_u32) (void)hipHostFree(h->h_u32);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -788,8 +788,8 @@ extern "C" int forword_gpu_init(forword_gpu_t **out, const void *data, size_t da
         dalloc(h, (void **)&h->d_pss, ((size_t)n / 16 + 64) * 4, "norm partials") ||
         dalloc(h, (void **)&h->d_scale, 64, "norm scale") || dalloc(h, (void **)&h->d_ticket, 64, "norm ticket"))
         FAIL();
-    if (hipHostMalloc((void **)&h->h_state, sizeof(StepState), 0) != hipSuccess ||
-        hipHostMalloc((void **)&h->h_logits, (size_t)c.n_vocab * 4, 0) != hipSuccess ||
+    h->h_state = &h->host_state;
+    if (hipHostMalloc((void **)&h->h_logits, (size_t)c.n_vocab * 4, 0) != hipSuccess ||
         hipHostMalloc((void **)&h->h_u32, 4 * 4, 0) != hipSuccess) {
         set_err("pinned host allocation failed");
         FAIL();
@@ -827,7 +827,7 @@ static int step_once(forword_gpu_t *h, uint32_t token, size_t pos)
     h->h_state->pos = (uint32_t)pos;
     h->h_state->n_prompt = 0;
     h->h_state->greedy = 0;
-    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    HIPCHK(launch_set_state(h->d_state, *h->h_state, h->stream), "state upload");
     if (run_steps(h, 1)) return -1;
     h->traced = true;
     return 0;
@@ -871,7 +871,7 @@ extern "C" int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *pro
     h->h_state->n_prompt = (uint32_t)n_prompt;
     h->h_state->next = 0;
     h->h_state->greedy = 1;
-    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    HIPCHK(launch_set_state(h->d_state, *h->h_state, h->stream), "state upload");
     if (run_steps(h, n_fwd)) return -1;
     if (n_gen) HIPCHK(hipMemcpyAsync(out_ids, h->d_ids, n_gen * 4, hipMemcpyDeviceToHost, h->stream), "ids download");
     HIPCHK(hipStreamSynchronize(h->stream), "generate_greedy");
@@ -911,7 +911,7 @@ extern "C" int forword_gpu_decode_from(forword_gpu_t *h, uint32_t token, size_t 
     h->h_state->n_prompt = (uint32_t)(pos + 1);
     h->h_state->next = 0;
     h->h_state->greedy = 1;
-    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    HIPCHK(launch_set_state(h->d_state, *h->h_state, h->stream), "state upload");
     if (run_steps(h, n_steps)) return -1;
     h->h_state->pos = (uint32_t)(pos + n_steps);
     h->traced = true;
@@ -1102,7 +1102,7 @@ extern "C" int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, si
     h->h_state->n_prompt = (uint32_t)n_prompt;
     h->h_state->next = 0;
     h->h_state->greedy = 1;
-    HIPCHK(hipMemcpyAsync(h->d_state, h->h_state, sizeof(StepState), hipMemcpyHostToDevice, h->stream), "state upload");
+    HIPCHK(launch_set_state(h->d_state, *h->h_state, h->stream), "state upload");
     if (run_steps(h, n_prompt)) return -1;
     // main.c:173-217: sample from the logits on the device, forward the sample
     for (size_t g = 0; g < n_gen; g++) {

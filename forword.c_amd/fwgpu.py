@@ -61,19 +61,20 @@ class SynthSpec(C.Structure):
     _fields_ = [("n_embd", u32), ("n_ff", u32), ("n_layer", u32), ("n_head", u32), ("n_head_kv", u32),
                 ("n_vocab", u32), ("n_ctx", u32), ("rope_freq_base", f32), ("norm_eps", f32),
                 ("linear_type", u32), ("embd_type", u32), ("output_type", u32), ("seed", u64),
-                ("w_std", f32), ("norm_std", f32), ("threads", u32), ("arch", u32)]
+                ("w_std", f32), ("norm_std", f32), ("threads", u32), ("arch", u32), ("mix_type", u32)]
 
 
 def spec(n_embd, n_ff, n_layer, n_head, n_head_kv, n_vocab, n_ctx, rope_freq_base=10000.0,
          norm_eps=1e-5, linear_type=GGML_Q8_0, embd_type=GGML_Q8_0, output_type=GGML_Q8_0,
-         seed=1, w_std=0.02, norm_std=0.01, threads=0, arch="llama") -> SynthSpec:
+         seed=1, w_std=0.02, norm_std=0.01, threads=0, arch="llama", mix_type=0) -> SynthSpec:
     """Synthetic model shape.  arch "qwen2" adds attn_{q,k,v}.bias per layer; "gemma"
     (gated GELU-tanh FFN, embedding times sqrt(n_embd)) ties the lm-head to token_embd;
     "phi2" is the LayerNorm / parallel-residual / plain-FFN / NEOX-RoPE block with norm
-    and output-projection biases."""
+    and output-projection biases.  mix_type != 0 gives attn_v and ffn_down of the even
+    layers that type instead of linear_type."""
     return SynthSpec(n_embd, n_ff, n_layer, n_head, n_head_kv, n_vocab, n_ctx, rope_freq_base,
                      norm_eps, linear_type, embd_type, output_type, seed, w_std, norm_std, threads,
-                     SYNTH_ARCHS[arch])
+                     SYNTH_ARCHS[arch], mix_type)
 
 
 # Workload shapes (dims, heads, ffn, vocab, RoPE base) of the configurations this path is measured on.

@@ -397,7 +397,9 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         !fwh_block_bytes(s->linear_type) || !fwh_block_bytes(s->embd_type) ||
         !fwh_block_bytes(s->output_type) || s->n_embd % fwh_block_values(s->linear_type) ||
         s->n_ff % fwh_block_values(s->linear_type) || s->n_embd % fwh_block_values(s->embd_type) ||
-        s->n_embd % fwh_block_values(s->output_type))
+        s->n_embd % fwh_block_values(s->output_type) ||
+        (s->mix_type && (!fwh_block_bytes(s->mix_type) || s->n_embd % fwh_block_values(s->mix_type) ||
+                         s->n_ff % fwh_block_values(s->mix_type))))
         return -1;
     uint64_t hd = s->n_embd / s->n_head, kvd = hd * s->n_head_kv;
     const int phi2 = s->arch == FORWORD_ARCH_PHI2;
@@ -410,6 +412,7 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
     add_t(L, "token_embd.weight", T_EMBD, s->embd_type, s->n_embd, s->n_vocab, 2);
     if (gpt2) add_t(L, "position_embd.weight", T_EMBD, s->embd_type, s->n_embd, s->n_ctx, 2);
     for (uint32_t l = 0; l < s->n_layer; l++) {
+        const uint32_t mixed = s->mix_type && l % 2 == 0 ? s->mix_type : s->linear_type;
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l); add_t(L, nm, T_ATTN_NORM, FORWORD_GGML_F32, s->n_embd, 1, 1);
         if (ln) BIAS("blk.%u.attn_norm.bias", s->n_embd);
         if (gpt2) {                                   /* one [q | k | v] projection (attention.c:68-96) */
@@ -418,7 +421,7 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         } else {
             snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); add_t(L, nm, T_Q, s->linear_type, s->n_embd, s->n_embd, 2);
             snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); add_t(L, nm, T_K, s->linear_type, s->n_embd, kvd, 2);
-            snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, s->linear_type, s->n_embd, kvd, 2);
+            snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); add_t(L, nm, T_V, mixed, s->n_embd, kvd, 2);
         }
         if (s->arch == FORWORD_ARCH_QWEN2) {
             BIAS("blk.%u.attn_q.bias", s->n_embd); BIAS("blk.%u.attn_k.bias", kvd); BIAS("blk.%u.attn_v.bias", kvd);
@@ -430,7 +433,7 @@ static int build_layout(const fwh_synth_spec_t *s, layout_t *L)
         if (!ln) { snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); add_t(L, nm, T_GATE, s->linear_type, s->n_embd, s->n_ff, 2); }
         snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l); add_t(L, nm, T_UP, s->linear_type, s->n_embd, s->n_ff, 2);
         if (gpt2) BIAS("blk.%u.ffn_up.bias", s->n_ff);
-        snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); add_t(L, nm, T_DOWN, s->linear_type, s->n_ff, s->n_embd, 2);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); add_t(L, nm, T_DOWN, mixed, s->n_ff, s->n_embd, 2);
         if (gpt2) BIAS("blk.%u.ffn_down.bias", s->n_embd);
     }
 #undef BIAS
@@ -490,6 +493,9 @@ typedef struct {
     uint8_t *data;          /* start of data section */
     size_t rows_per_job;
     size_t *job_first;      /* first global job index per tensor (n_t + 1 entries) */
+    size_t n_jobs;
+    int progress;           /* env FW_SYNTH_PROGRESS: a line on stderr per tenth done */
+    atomic_size_t done;
 } gen_ctx_t;
 
 static void gen_job(void *vctx, size_t job)
@@ -513,6 +519,11 @@ static void gen_job(void *vctx, size_t job)
         fwh_quantize(t->type, buf, t->cols, c->data + t->offset + r * row_bytes);
     }
     free(buf);
+    if (c->progress) {
+        const size_t d = atomic_fetch_add(&c->done, 1) + 1;
+        if (d * 10 / c->n_jobs != (d - 1) * 10 / c->n_jobs)
+            fprintf(stderr, "fwh_synth: %zu%% of %zu row blocks written\n", d * 100 / c->n_jobs, c->n_jobs);
+    }
 }
 
 size_t fwh_synth_size(const fwh_synth_spec_t *spec)
@@ -570,11 +581,13 @@ size_t fwh_synth_write(const fwh_synth_spec_t *spec, void *out, size_t cap)
         uint64_t next = i + 1 < L.n_t ? L.t[i + 1].offset : (L.total - L.data_offset);
         if (next > end) memset(data + end, 0, (size_t)(next - end));
     }
-    gen_ctx_t c = { &L, data, 64, NULL };
+    gen_ctx_t c = { &L, data, 64, NULL, 0, 0, 0 };
     c.job_first = (size_t *)calloc(L.n_t + 1, sizeof(size_t));
     for (size_t i = 0; i < L.n_t; i++)
         c.job_first[i + 1] = c.job_first[i] + (L.t[i].rows + c.rows_per_job - 1) / c.rows_per_job;
-    run_parallel(gen_job, &c, c.job_first[L.n_t], s->threads);
+    c.n_jobs = c.job_first[L.n_t];
+    c.progress = getenv("FW_SYNTH_PROGRESS") != NULL;
+    run_parallel(gen_job, &c, c.n_jobs, s->threads);
     free(c.job_first);
     size_t total = L.total;
     free(L.t);

@@ -103,6 +103,9 @@ typedef struct {
                                      (attn, ffn, output) and to attn_output; GPT2 as phi2
                                      plus position_embd, one attn_qkv (+bias), ffn_up/down
                                      biases and no output.weight (n_head_kv must equal n_head) */
+    uint32_t mix_type;            /* 0 = every linear is linear_type; else attn_v and ffn_down of
+                                     the even layers are this type (the per-tensor mix of
+                                     llama.cpp's *_M files, e.g. Q6_K among Q4_K) */
 } fwh_synth_spec_t;
 
 /* Exact byte size of the GGUF image fwh_synth_write would produce. */

@@ -180,12 +180,17 @@ class OracleModel:
 
     def kv(self, layer: int, pos: int):
         kvd = self.host.cfg.n_head_kv * self.host.cfg.head_dim
+        if not (0 <= layer < self.host.cfg.n_layer and 0 <= pos < self.host.n_ctx):
+            raise ValueError("kv: row outside the cache")
         k = np.ctypeslib.as_array(lib().fwc_kv_k(self.m, layer, pos), shape=(kvd,)).copy()
         v = np.ctypeslib.as_array(lib().fwc_kv_v(self.m, layer, pos), shape=(kvd,)).copy()
         return k, v
 
     def set_kv(self, layer: int, pos0: int, k: np.ndarray, v: np.ndarray):
         kvd = self.host.cfg.n_head_kv * self.host.cfg.head_dim
+        if not 0 <= layer < self.host.cfg.n_layer or pos0 < 0 or pos0 + k.shape[0] > self.host.n_ctx or \
+                k.shape != v.shape or k.shape[1:] != (kvd,):
+            raise ValueError("set_kv: rows outside the cache or of the wrong width")
         for i in range(k.shape[0]):
             np.ctypeslib.as_array(lib().fwc_kv_k(self.m, layer, pos0 + i), shape=(kvd,))[:] = k[i]
             np.ctypeslib.as_array(lib().fwc_kv_v(self.m, layer, pos0 + i), shape=(kvd,))[:] = v[i]

@@ -93,3 +93,39 @@ def test_kquant_model_matches_oracle():
             lg = gm.prefill(prompt)
             assert fw_cpu.argmax(lg) == int(ref_gen[0])
             assert np.array_equal(gm.generate_greedy_batched(prompt, 6), ref_gen)
+
+
+def mixed_spec():
+    """The reference's own model layout (tensors.txt, a Q4_K_M file): Q4_K linears with
+    attn_v and ffn_down Q6_K on every other layer, n_ff an odd number of super-blocks
+    (1280 = 5 x 256), Q6_K output."""
+    return fwgpu.spec(512, 1280, 4, 8, 2, 2000, 96, 10000.0, linear_type=gs.Q4K, embd_type=gs.Q4K,
+                      output_type=gs.Q6K, seed=1313, mix_type=gs.Q6K)
+
+
+def test_mixed_type_layers_match_oracle():
+    """Per-tensor types that change inside a layer and from layer to layer:
+    per-token decode, the device-resident greedy loop and the batched prefill."""
+    prompt = np.random.default_rng(13).integers(3, 2000, 10).astype(np.uint32)
+    with fwgpu.HostModel(synth=mixed_spec()) as host, fw_cpu.OracleModel(host) as om:
+        assert host.tensor("blk.0.attn_v.weight").ggml_type == gs.Q6K
+        assert host.tensor("blk.1.attn_v.weight").ggml_type == gs.Q4K
+        assert host.tensor("blk.2.ffn_down.weight").ggml_type == gs.Q6K
+        assert host.tensor("blk.3.ffn_down.weight").ggml_type == gs.Q4K
+        with fwgpu.GpuModel(host) as gm:
+            toks = list(prompt)
+            for f in range(len(prompt) + 5):
+                exp = om.forward(int(toks[f]), f)
+                got = gm.forward(int(toks[f]), f)
+                check_close(got, exp, f"logits at forward {f}")
+                assert fw_cpu.argmax(got) == fw_cpu.argmax(exp)
+                if f + 1 >= len(toks):
+                    toks.append(fw_cpu.argmax(exp))
+            check_close(gm.layer_trace().reshape(-1), om.trace().reshape(-1), "residual stream")
+            ref_gen = np.array(toks[len(prompt):len(prompt) + 6], np.uint32)
+        with fwgpu.GpuModel(host) as gm:
+            assert np.array_equal(gm.generate_greedy(prompt, 6), ref_gen)
+        with fwgpu.GpuModel(host) as gm:
+            lg = gm.prefill(prompt)
+            assert fw_cpu.argmax(lg) == int(ref_gen[0])
+            assert np.array_equal(gm.generate_greedy_batched(prompt, 6), ref_gen)

@@ -130,3 +130,35 @@ def test_persistent_forward_after_greedy_and_errors():
         assert not gm.forward_raw(host.cfg.n_vocab, 0)
         nxt = gm.forward_argmax(int(first[0]), len(prompt))
         assert nxt == fw_cpu.argmax(om.forward(int(first[0]), len(prompt)))
+
+
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_phase"])
+def test_decode_from_after_kv_write_matches_oracle(persistent):
+    """decode_from right after kv_write has filled the whole cache and a forward:
+    the steps it queues start at the token and position the call names, also
+    when it only queues them and decode continues the loop."""
+    fw_cpu.set_threads(8)
+    with fwgpu.HostModel(synth=spec_of("hd64_g4_q4")) as host:
+        c, n = host.cfg, host.n_ctx
+        kvd = c.n_head_kv * c.head_dim
+        rng = np.random.default_rng(21)
+        rows = [(rng.standard_normal((n, kvd), dtype=np.float32), rng.standard_normal((n, kvd), dtype=np.float32))
+                for _ in range(c.n_layer)]
+        with fw_cpu.OracleModel(host) as om:
+            for layer, (k, v) in enumerate(rows):
+                om.set_kv(layer, 0, k, v)
+            ref = om.forward(17, 40)
+            t, exp = fw_cpu.argmax(ref), []
+            nxt = t
+            for i in range(6):
+                t = fw_cpu.argmax(om.forward(int(t), 41 + i))
+                exp.append(t)
+        ctx = per_phase_kernels() if not persistent else open(os.devnull)
+        with ctx, fwgpu.GpuModel(host) as gm:
+            assert gm.persistent == persistent
+            for layer, (k, v) in enumerate(rows):
+                gm.kv_write(layer, 0, k, v)
+            close(gm.forward(17, 40), ref, "logits at position 40")
+            assert np.array_equal(gm.decode_from(nxt, 41, 6), exp)
+            gm.decode_from(nxt, 41, 3, copy_out=False)
+            assert np.array_equal(gm.decode(3), exp[3:])
