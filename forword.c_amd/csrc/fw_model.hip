@@ -1355,6 +1355,66 @@ extern "C" int forword_gpu_attention(const float *q, const float *kc, const floa
                                      (uint32_t)pos, (hipStream_t)stream), "attention");
 }
 
+// ── allocation-free attention ────────────────────────────────────────────────
+// The split partials of forword_gpu_attention_noalloc live in `scratch`, one
+// copy per device for the life of the process.  Host code never passes the
+// symbol itself: its device address comes from hipGetSymbolAddress, looked up
+// once per device on the first call made with that device current.  Every
+// (head, split) entry a launch reads is written earlier in the same launch, so
+// nothing is cleared between calls; calls that overlap on one device race.
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / 4];
+std::mutex g_noalloc_mu;
+float *g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+float *noalloc_scratch()
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) {
+        set_err("attention_noalloc: no usable current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_err("attention_noalloc: scratch address lookup failed: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_noalloc_ptr[dev] = (float *)p;
+    }
+    return g_noalloc_ptr[dev];
+}
+} // namespace
+
+extern "C" int forword_gpu_attention_noalloc(const float *q, const float *kc, const float *vc, float *out,
+                                             size_t n_head, size_t n_kv, size_t hd, size_t n_ctx, size_t pos,
+                                             void *stream)
+{
+    if (!q || !kc || !vc || !out || !n_head || !n_kv || !hd || n_head % n_kv || pos >= n_ctx || n_ctx >= (1u << 31)) {
+        set_err("attention_noalloc: invalid head configuration or position");
+        return -1;
+    }
+    if (!attn_supported((uint32_t)hd, (uint32_t)(n_head / n_kv))) {
+        set_err("attention_noalloc: head_dim %zu / GQA group %zu not supported", hd, n_head / n_kv);
+        return -1;
+    }
+    const uint32_t ns = attn_splits((uint32_t)(pos + 1), (uint32_t)n_kv);
+    const size_t need = n_head * ns * (hd + 2) * 4;
+    if (need > kNoAllocScratchBytes) {
+        set_err("attention_noalloc: %zu heads x %u splits need %zu B of partials, above the %zu B scratch", n_head, ns,
+                need, kNoAllocScratchBytes);
+        return -1;
+    }
+    float *part = noalloc_scratch();
+    if (!part) return -1;
+    return launched(launch_attention(q, kc, vc, part, out, (uint32_t)n_head, (uint32_t)n_kv, (uint32_t)hd, ns, nullptr,
+                                     (uint32_t)pos, (hipStream_t)stream), "attention_noalloc");
+}
+
 extern "C" int forword_gpu_silu_mul(const float *g, const float *u, float *out, size_t n, void *stream)
 {
     if (!g || !u || !out) { set_err("silu_mul: invalid arguments"); return -1; }

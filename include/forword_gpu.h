@@ -282,6 +282,20 @@ int forword_gpu_attention(const float *q, const float *k_cache, const float *v_c
                           float *out, size_t n_head, size_t n_head_kv, size_t head_dim,
                           size_t n_ctx, size_t pos, void *stream);
 
+/*
+ * forword_gpu_attention without allocating: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, validation and results as forword_gpu_attention; the split
+ * partials (n_head x splits x (head_dim + 2) floats, splits as that call
+ * chooses them) live in a fixed 8 MiB device array per GPU, and a call whose
+ * partials exceed it returns -1.  The array is shared by every call on that
+ * GPU: calls that overlap on one GPU race.
+ */
+int forword_gpu_attention_noalloc(const float *q, const float *k_cache, const float *v_cache,
+                                  float *out, size_t n_head, size_t n_head_kv, size_t head_dim,
+                                  size_t n_ctx, size_t pos, void *stream);
+
 /* out = silu(gate) * up, n elements (ffn.c:88-91,103-104 with apply_silu ffn.c:17-25). */
 int forword_gpu_silu_mul(const float *gate, const float *up, float *out, size_t n, void *stream);
 
