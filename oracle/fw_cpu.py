@@ -11,7 +11,7 @@ import sys
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "libfwcpu.so")
+LIB = os.environ.get("FW_CPU_LIB") or os.path.join(HERE, "libfwcpu.so")   # override: instrumented builds
 sys.path.insert(0, os.path.join(os.path.dirname(HERE), "forword.c_amd"))
 import fwgpu  # noqa: E402  (struct layouts of the C ABI)
 

@@ -52,20 +52,26 @@ def gold_model(name):
     return load_npz(f"model_{name}.npz")
 
 
-def check_logit_stats(lg, row, f, atol=2e-3, rtol=1e-3):
+def check_logit_stats(lg, row, f, atol=2e-3, rtol=1e-3, strict=True):
     """A reference-written statistics row of one forward (ref_driver's gen mode:
     argmax, max logit, largest logit at another index, their difference, double
     sum of all logits) against logits `lg`, each within what the per-logit bar
-    |got - exp| <= atol + rtol |exp| allows."""
+    |got - exp| <= atol + rtol |exp| allows.  With strict=False (a forward whose
+    argmax feeds nothing, e.g. inside a prompt) another argmax is accepted when
+    the expected top two are closer than that bar."""
     best = int(np.argmax(lg))
-    assert best == int(row[0]), f"greedy choice differs at forward {f}"
+    tol = lambda x: atol + rtol * abs(x)
+    tie = best != int(row[0])
+    if tie:
+        assert not strict, f"greedy choice differs at forward {f}"
+        assert row[3] <= tol(row[1]) + tol(row[2]), f"argmax differs at forward {f} beyond a near-tie"
     rest = lg.astype(np.float64)
     rest[best] = -np.inf
     second = float(rest.max())
-    tol = lambda x: atol + rtol * abs(x)
-    assert abs(float(lg[best]) - row[1]) <= tol(row[1]), f"max logit at forward {f}: {lg[best]} vs {row[1]}"
-    assert abs(second - row[2]) <= tol(row[2]), f"runner-up at forward {f}: {second} vs {row[2]}"
-    assert abs((float(lg[best]) - second) - row[3]) <= tol(row[1]) + tol(row[2]), f"margin at forward {f}"
+    k = 2 if tie else 1
+    assert abs(float(lg[best]) - row[1]) <= k * tol(row[1]), f"max logit at forward {f}: {lg[best]} vs {row[1]}"
+    assert abs(second - row[2]) <= k * tol(row[2]), f"runner-up at forward {f}: {second} vs {row[2]}"
+    assert abs((float(lg[best]) - second) - row[3]) <= k * (tol(row[1]) + tol(row[2])), f"margin at forward {f}"
     sum_tol = lg.size * atol + rtol * float(np.abs(lg.astype(np.float64)).sum())
     got_sum = float(np.sum(lg, dtype=np.float64))
     assert abs(got_sum - row[4]) <= sum_tol, f"logit sum at forward {f}: {got_sum} vs {row[4]}"
