@@ -21,7 +21,8 @@ Prints one JSON line:
 Other modes: --config lc (8B shape at 32K context, KV rows 0..32767 written
 with N(0,1) through kv_write, then greedy decode), --config 70b, --mode decode
 (just the timed decode, for profilers), --mode copy (device-to-device copy of
-known size: calibrates the memory-traffic counters).
+known size: calibrates the memory-traffic counters), --mode micro (only the
+quant_matvec microbenchmark, for profiling k_gemv).
 """
 from __future__ import annotations
 
@@ -65,6 +66,15 @@ class Hip:
         fwgpu._sig(L, "hipEventElapsedTime", C.c_int, [C.POINTER(C.c_float), C.c_void_p, C.c_void_p])
         fwgpu._sig(L, "hipStreamSynchronize", C.c_int, [C.c_void_p])
         fwgpu._sig(L, "hipMemcpyAsync", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p])
+        vpp = C.POINTER(C.c_void_p)
+        fwgpu._sig(L, "hipStreamCreate", C.c_int, [vpp])
+        fwgpu._sig(L, "hipStreamDestroy", C.c_int, [C.c_void_p])
+        fwgpu._sig(L, "hipStreamBeginCapture", C.c_int, [C.c_void_p, C.c_int])
+        fwgpu._sig(L, "hipStreamEndCapture", C.c_int, [C.c_void_p, vpp])
+        fwgpu._sig(L, "hipGraphInstantiate", C.c_int, [vpp, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t])
+        fwgpu._sig(L, "hipGraphLaunch", C.c_int, [C.c_void_p, C.c_void_p])
+        fwgpu._sig(L, "hipGraphExecDestroy", C.c_int, [C.c_void_p])
+        fwgpu._sig(L, "hipGraphDestroy", C.c_int, [C.c_void_p])
 
     def event(self):
         e = C.c_void_p()
@@ -82,6 +92,20 @@ class Hip:
 
     def sync(self, stream):
         assert self.L.hipStreamSynchronize(stream) == 0
+
+    def stream(self):
+        s = C.c_void_p()
+        assert self.L.hipStreamCreate(C.byref(s)) == 0
+        return s
+
+    def graph_of(self, stream, enqueue):
+        """enqueue(stream) captured (thread-local mode) as an executable graph."""
+        assert self.L.hipStreamBeginCapture(stream, 1) == 0
+        enqueue(stream)
+        g, ex = C.c_void_p(), C.c_void_p()
+        assert self.L.hipStreamEndCapture(stream, C.byref(g)) == 0
+        assert self.L.hipGraphInstantiate(C.byref(ex), g, None, None, 0) == 0
+        return g, ex
 
 
 def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34):
@@ -130,35 +154,51 @@ def timed_decode(hip, gm, steps):
 
 def microbench(hip, min_bytes=1 << 30, reps=48):
     """quant_matvec (operator entry point) GB/s at the microbenchmark shapes: `reps`
-    back-to-back calls over rotating weight copies (>= 1 GiB, so the 256 MB
-    last-level cache cannot serve repeats), one event pair around all of them."""
+    calls over rotating weight copies (>= 1 GiB, so the 256 MB last-level cache cannot
+    serve repeats), timed with one event pair around all of them, once as plain
+    back-to-back launches and once replayed from a captured graph (fewer launch gaps)."""
     L = fwgpu.gpu_lib()
     out = []
     x = fwgpu.DeviceBuffer.from_array(fwgpu.randn(7, 14336))
     y = fwgpu.DeviceBuffer(14336 * 4)
+    st = hip.stream()
     for t in (fwgpu.GGML_Q4_0, fwgpu.GGML_Q5_0, fwgpu.GGML_Q8_0):
         for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
             w = fwgpu.synth_matrix(t, rows, cols, seed=100 + t)
             copies = max(2, -(-min_bytes // w.nbytes))
             bufs = [fwgpu.DeviceBuffer.from_array(w) for _ in range(copies)]
             algo = w.nbytes + 4 * cols + 4 * rows
-            for i in range(copies):                                 # warm-up pass
-                assert L.forword_gpu_quant_matvec(bufs[i].ptr, w.nbytes, t, x.ptr, y.ptr, cols, rows, None) == 0
-            hip.sync(None)
+
+            def enqueue(stream, n=reps):
+                for i in range(n):
+                    assert L.forword_gpu_quant_matvec(bufs[i % copies].ptr, w.nbytes, t, x.ptr, y.ptr,
+                                                      cols, rows, stream) == 0
+
+            enqueue(st, copies)                                     # warm-up pass
+            hip.sync(st)
             e0, e1 = hip.event(), hip.event()
-            hip.record(e0, None)
-            for i in range(reps):
-                assert L.forword_gpu_quant_matvec(bufs[i % copies].ptr, w.nbytes, t, x.ptr, y.ptr,
-                                                  cols, rows, None) == 0
-            hip.record(e1, None)
-            hip.sync(None)
+            hip.record(e0, st)
+            enqueue(st)
+            hip.record(e1, st)
+            us_launch = hip.ms(e0, e1) * 1e3 / reps
+            g, ex = hip.graph_of(st, enqueue)
+            assert hip.L.hipGraphLaunch(ex, st) == 0                # warm-up replay
+            hip.sync(st)
+            hip.record(e0, st)
+            assert hip.L.hipGraphLaunch(ex, st) == 0
+            hip.record(e1, st)
             us = hip.ms(e0, e1) * 1e3 / reps
+            hip.L.hipGraphExecDestroy(ex)
+            hip.L.hipGraphDestroy(g)
             for b in bufs:
                 b.free()
             gbs = algo / (us * 1e-6) / 1e9
             out.append({"type": fwgpu.TYPE_NAMES[t], "rows": rows, "cols": cols, "bytes": algo,
-                        "us_per_call": round(us, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
-            log(f"microbench {fwgpu.TYPE_NAMES[t]} {rows}x{cols}: {us:.2f} us per call, {gbs:.0f} GB/s")
+                        "us_per_call": round(us, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "us_per_call_launched": round(us_launch, 2)})
+            log(f"microbench {fwgpu.TYPE_NAMES[t]} {rows}x{cols}: {us:.2f} us per call from a graph "
+                f"({us_launch:.2f} launched), {gbs:.0f} GB/s")
+    hip.L.hipStreamDestroy(st)
     x.free()
     y.free()
     return out
@@ -247,7 +287,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "qwen2-7b", "phi2", "gpt2-xl", "tiny"])
-    ap.add_argument("--mode", default="full", choices=["full", "decode", "copy"])
+    ap.add_argument("--mode", default="full", choices=["full", "decode", "copy", "micro"])
     ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -260,6 +300,9 @@ def main():
     hip = Hip()
     if args.mode == "copy":
         copy_calibration(hip, args.copy_mb)
+        return
+    if args.mode == "micro":
+        print(json.dumps({"microbench": microbench(hip)}), flush=True)
         return
 
     lc = args.config == "lc"

@@ -99,6 +99,11 @@ hipError_t launch_attention(const float *q, const float *kc, const float *vc, fl
                             uint32_t n_head, uint32_t n_kv, uint32_t head_dim, uint32_t n_splits,
                             const StepState *st, uint32_t pos_host, hipStream_t s);
 
+// y = W x for Q4_0 / Q5_0 / Q8_0 rows of whole block pairs (fw_gemv.hip);
+// hipErrorNotSupported for other types, shapes or alignments (the caller then
+// uses the general kernel).
+hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t row_bytes, const float *x, float *y, uint32_t n_rows,
+                       uint32_t n_cols, hipStream_t s);
 hipError_t launch_set_state(StepState *st, const StepState &v, hipStream_t s);
 hipError_t launch_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *counter,
                          uint32_t *out, StepState *st, const uint32_t *prompt, uint32_t *ids,

@@ -88,10 +88,4 @@ int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes
 hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,
                      hipStream_t s);
 
-// y = W x (one Q4_0/Q5_0/Q8_0 matrix of n_rows x n_cols, rows row_bytes apart)
-// with the step kernel's GEMV machinery; hipErrorNotSupported for shapes it
-// does not take (the caller then uses the general kernel).
-hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t row_bytes, const float *x, float *y, uint32_t n_rows,
-                       uint32_t n_cols, hipStream_t s);
-
 } // namespace fw

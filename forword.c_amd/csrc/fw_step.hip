@@ -1257,49 +1257,6 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     }
 }
 
-// ── standalone matrix-vector product ────────────────────────────────────────
-
-// y = W x for one Q4_0/Q5_0/Q8_0 matrix (quant_matvec, quant_matvec.c:263-312),
-// with the machinery of a phase of the step kernel: one 512-thread workgroup
-// per CU, rows split evenly over the workgroups, the first weight items issued
-// before x is staged, weight rings in LDS, DPP row sums.  x and y are plain
-// buffers (the launch orders them).
-template <uint32_t T>
-__global__ __launch_bounds__(MK_THREADS) void k_gemv(const uint8_t *w, uint64_t row_bytes, const float *x, float *y,
-                                                     uint32_t n_rows, uint32_t n_cols, uint32_t fixed)
-{
-    extern __shared__ __align__(16) float lds[];
-    uint8_t *lds8 = reinterpret_cast<uint8_t *>(lds);
-    MkGemv g{};
-    g.w[0] = w;
-    g.rows[0] = g.n_rows = n_rows;
-    g.n_cols = n_cols;
-    g.row_bytes = row_bytes;
-    // x loads first, then the first weight items: loads complete in order, so
-    // the other way round x (and every product) would wait for all the items.
-    constexpr int XB = 16;                              // float2 per thread per batch
-    const FW_GLOBAL float2v *x2 = reinterpret_cast<const FW_GLOBAL float2v *>(gptr(x));
-    const uint32_t t = tid(), n2 = n_cols / 2;
-    uint32_t n_pre = 0;
-    for (uint32_t j0 = 0; j0 < n2; j0 += XB * MK_THREADS) {
-        float2v v[XB];
-#pragma unroll
-        for (int b = 0; b < XB; b++)
-            if (j0 + t + b * MK_THREADS < n2) v[b] = x2[j0 + t + b * MK_THREADS];
-        if (j0 == 0) n_pre = prefetch<T, 1>(g, lds8, fixed, 0);
-#pragma unroll
-        for (int b = 0; b < XB; b++)
-            if (j0 + t + b * MK_THREADS < n2) *reinterpret_cast<float2v *>(lds + swz(2 * (j0 + t + b * MK_THREADS))) = v[b];
-    }
-    __syncthreads();
-    float *part = lds + fixed / 4;
-    gemv<T, 1>(g, lds, part, lds8, fixed, 0, n_pre);
-    uint32_t lo, hi;
-    wg_rows(n_rows, lo, hi);
-    const uint32_t ns = n_slices(n_cols);
-    for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) y[lo + rl] = row_sum<1>(part, rl, 0, ns);
-}
-
 // ── host side ───────────────────────────────────────────────────────────────
 
 static bool mk_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
@@ -1365,35 +1322,6 @@ hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, 
     MkArgs arg = a;
     void *params[] = { &arg };
     return hipLaunchCooperativeKernel((const void *)k, dim3(n_wg), dim3(MK_THREADS), params, (unsigned)lds_bytes, s);
-}
-
-
-// y = W x through k_gemv; hipErrorNotSupported when the shape does not suit it
-// (columns not a multiple of 64, misaligned rows, LDS too small).
-hipError_t launch_gemv(uint32_t type, const uint8_t *w, uint64_t row_bytes, const float *x, float *y, uint32_t n_rows,
-                       uint32_t n_cols, hipStream_t s)
-{
-    if (!mk_type_ok(type) || n_cols % 64 || row_bytes % 4 || ((uintptr_t)w & 3) || ((uintptr_t)x & 7)) return hipErrorNotSupported;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus < 1)
-        return hipErrorNotSupported;
-    const uint32_t n_wg = (uint32_t)cus;
-    const uint32_t part = (mk_rows_per_wg(n_rows, n_wg) * n_slices(n_cols) + 3) & ~3u;
-    if ((size_t)4 * part + 4 * (size_t)n_cols + 16 > MK_LDS_BYTES) return hipErrorNotSupported;
-    const uint32_t fixed = (MK_LDS_BYTES - 4 * part) & ~15u;
-    if (ring_slots(ring_wave_bytes(fixed, ring_base(n_cols, 0)), type, 1) < 1) return hipErrorNotSupported;
-    typedef void (*kt)(const uint8_t *, uint64_t, const float *, float *, uint32_t, uint32_t, uint32_t);
-    const kt k = type == kQ4_0 ? (kt)k_gemv<kQ4_0> : type == kQ5_0 ? (kt)k_gemv<kQ5_0> : (kt)k_gemv<kQ8_0>;
-    static bool attr_set[3] = { false, false, false };
-    const int ti = type == kQ4_0 ? 0 : type == kQ5_0 ? 1 : 2;
-    if (!attr_set[ti]) {
-        if (hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)MK_LDS_BYTES) != hipSuccess)
-            return hipErrorNotSupported;
-        attr_set[ti] = true;
-    }
-    hipLaunchKernelGGL(k, dim3(n_wg), dim3(MK_THREADS), MK_LDS_BYTES, s, w, row_bytes, x, y, n_rows, n_cols, fixed);
-    return hipGetLastError();
 }
 
 } // namespace fw

@@ -25,7 +25,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBDIR = os.path.join(HERE, "lib")
 HOST_LIB = os.environ.get("FW_HOST_LIB") or os.path.join(LIBDIR, "libfw_host.so")   # override: instrumented builds
-GPU_LIB = os.path.join(LIBDIR, "libforword_gpu.so")
+GPU_LIB = os.environ.get("FW_GPU_LIB") or os.path.join(LIBDIR, "libforword_gpu.so")   # override: A/B builds
 
 GGML_F32, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 2, 6, 8, 12, 14
 BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q5_0: 22, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q6_K: 210}
