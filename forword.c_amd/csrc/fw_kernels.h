@@ -136,7 +136,7 @@ hipError_t launch_silu(const float *x, float *out, uint64_t n, hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);
 
 // Device-resident sampling (fw_sample.hip): the xorshift64 state of the
-// generation loop and an error flag (nucleus larger than the candidate buffer).
+// generation loop and an error flag (a top-p decision without any candidate).
 struct SampleState {
     uint64_t rng;
     uint32_t err;
@@ -146,11 +146,13 @@ struct SampleState {
 uint32_t samp_blocks(uint32_t n);
 // One decision on logits[n]: repetition penalty by history counts, greedy
 // (temperature <= 0) or top-p; the token goes to ids[g], st->token and counts.
-// buf: n floats; part: 512 floats; bcnt/bsum: 1024 zeroed buckets (cleared again).
+// buf: n floats; part: 512 floats; bcnt/bsum: 1024 zeroed buckets (cleared again);
+// gkeys: the next power of two >= n 64-bit keys (candidates beyond the cap that
+// the LDS sort holds are sorted there).
 hipError_t launch_sample(const float *logits, uint32_t n, const uint32_t *counts, float temperature, float top_p,
-                         float penalty, float *buf, float *part, uint32_t *bcnt, float *bsum, uint32_t cap,
-                         SampleState *ss, StepState *st, uint32_t *ids, uint32_t g, uint32_t *counts_rw,
-                         hipStream_t s);
+                         float penalty, float *buf, float *part, uint32_t *bcnt, unsigned long long *bsum,
+                         uint64_t *gkeys, uint32_t cap, SampleState *ss, StepState *st, uint32_t *ids, uint32_t g,
+                         uint32_t *counts_rw, hipStream_t s);
 
 // Batched prompt forward (fw_prefill.hip).
 // Up to three weight matrices of one type and column count computed as one

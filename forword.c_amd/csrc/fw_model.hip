@@ -157,7 +157,9 @@ struct forword_gpu {
     uint32_t prof_steps = 0;
     // sampled generation (allocated on first use): probabilities, reductions, buckets,
     // history counts, PRNG state, sampled ids
-    float *d_sbuf = nullptr, *d_spart = nullptr, *d_bsum = nullptr;
+    float *d_sbuf = nullptr, *d_spart = nullptr;
+    unsigned long long *d_bsum = nullptr;           // bucket weights, 2^-40 units
+    uint64_t *d_gkeys = nullptr;                     // top-p candidates beyond the LDS sort
     uint32_t *d_bcnt = nullptr, *d_counts = nullptr, *d_sids = nullptr;
     SampleState *d_ss = nullptr;
     // batched prefill: activations of up to kPrefillChunk tokens (allocated on first use)
@@ -1063,7 +1065,14 @@ extern "C" int forword_gpu_prefill_argmax(forword_gpu_t *h, const uint32_t *toke
 
 // ── sampled generation ───────────────────────────────────────────────────────
 
-// Candidates the top-p sort holds (LDS of one workgroup).
+static uint32_t next_pow2(uint32_t n)
+{
+    uint32_t p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+// Candidates the top-p sort holds in LDS; more go to the global key buffer.
 static constexpr uint32_t kSampleCap = 16384;
 
 extern "C" int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
@@ -1079,13 +1088,14 @@ extern "C" int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, si
     if (!h->d_sbuf) {
         if (dalloc(h, (void **)&h->d_sbuf, (size_t)nv * 4, "sampler probabilities") ||
             dalloc(h, (void **)&h->d_spart, 512 * 4, "sampler partials") ||
-            dalloc(h, (void **)&h->d_bsum, 1024 * 4, "sampler buckets") ||
+            dalloc(h, (void **)&h->d_bsum, 1024 * 8, "sampler buckets") ||
+            dalloc(h, (void **)&h->d_gkeys, (size_t)next_pow2(nv) * 8, "sampler keys") ||
             dalloc(h, (void **)&h->d_bcnt, 1024 * 4, "sampler buckets") ||
             dalloc(h, (void **)&h->d_counts, (size_t)nv * 4, "history counts") ||
             dalloc(h, (void **)&h->d_sids, (h->n_ctx + 1) * 4, "sampled ids") ||
             dalloc(h, (void **)&h->d_ss, sizeof(SampleState), "sampler state"))
             return -1;
-        HIPCHK(hipMemset(h->d_bsum, 0, 1024 * 4), "sampler buckets");
+        HIPCHK(hipMemset(h->d_bsum, 0, 1024 * 8), "sampler buckets");
         HIPCHK(hipMemset(h->d_bcnt, 0, 1024 * 4), "sampler buckets");
     }
     // history counts of the prompt (main.c:157-161) and the PRNG seed (main.c:98-99)
@@ -1107,7 +1117,7 @@ extern "C" int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, si
     // main.c:173-217: sample from the logits on the device, forward the sample
     for (size_t g = 0; g < n_gen; g++) {
         HIPCHK(launch_sample(h->d_logits, nv, h->d_counts, temperature, top_p, repetition_penalty, h->d_sbuf,
-                             h->d_spart, h->d_bcnt, h->d_bsum, kSampleCap, h->d_ss, h->d_state, h->d_sids,
+                             h->d_spart, h->d_bcnt, h->d_bsum, h->d_gkeys, kSampleCap, h->d_ss, h->d_state, h->d_sids,
                              (uint32_t)g, h->d_counts, h->stream),
                "sampler launch");
         if (g + 1 < n_gen && run_steps(h, 1)) return -1;
@@ -1119,7 +1129,7 @@ extern "C" int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, si
     h->h_state->pos = (uint32_t)n_fwd;
     h->traced = true;
     if (ss.err) {
-        set_err("generate: a top-p nucleus did not fit the %u-candidate sort (lower top_p or temperature)", kSampleCap);
+        set_err("generate: no finite probability to sample from (non-finite logits)");
         return -1;
     }
     return 0;

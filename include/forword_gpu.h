@@ -139,8 +139,9 @@ int forword_gpu_generate_greedy(forword_gpu_t *h, const uint32_t *prompt, size_t
  * stop-string check (main.c:190-208 is the caller's): out_ids[0..n_gen) are the
  * drawn tokens.  Draws equal the reference's except where the random number
  * falls within float rounding of a cumulative-probability boundary (the softmax
- * normaliser is a parallel sum).  -1 when a top-p nucleus holds more than 16384
- * tokens.  Costs n_prompt + n_gen - 1 forwards.
+ * normaliser is a parallel sum).  Any nucleus size, up to the whole vocabulary
+ * (large ones are sorted in a device buffer of the next power of two >= n_vocab
+ * keys).  Costs n_prompt + n_gen - 1 forwards.
  */
 int forword_gpu_generate(forword_gpu_t *h, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                          float temperature, float top_p, float repetition_penalty, uint64_t seed,

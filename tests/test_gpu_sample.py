@@ -43,11 +43,30 @@ def test_sampled_generation_repeats_bitwise():
         assert all(np.array_equal(runs[0], r) for r in runs[1:])
 
 
-def test_sampled_generation_nucleus_too_large():
-    # tiny model: 32000 near-uniform logits, top_p 0.99 needs ~31700 tokens
+def test_sampled_generation_large_nucleus_matches_oracle():
+    # tiny model: 32000 near-uniform logits, top_p 0.99 needs ~31700 candidates,
+    # more than the LDS sort holds: the global-buffer sort takes them
     m = gs.MODELS["tiny"]
-    with fwgpu.HostModel(synth=m["spec"]()) as host, fwgpu.GpuModel(host) as gm:
-        with pytest.raises(fwgpu.ForwordError):
-            gm.generate(gs.prompt("tiny"), 4, 1.0, 0.99, 1.0, 9)
-        assert "nucleus" in fwgpu.last_error()
-        gm.generate(gs.prompt("tiny"), 4, 0.0, 0.9, 1.1, 9)          # still usable
+    prompt = gs.prompt("tiny")
+    with fwgpu.HostModel(synth=m["spec"]()) as host, fw_cpu.OracleModel(host) as om:
+        exp = om.generate_sampled(prompt, 4, 1.0, 0.99, 1.0, 9)
+        with fwgpu.GpuModel(host) as gm:
+            got = gm.generate(prompt, 4, 1.0, 0.99, 1.0, 9)
+            again = gm.generate(prompt, 4, 1.0, 0.99, 1.0, 9)
+            gm.generate(prompt, 4, 0.0, 0.9, 1.1, 9)                  # the greedy path after it
+    assert np.array_equal(got, exp), (got, exp)
+    assert np.array_equal(got, again)
+
+
+def test_sampled_generation_full_vocabulary_nucleus():
+    # a 128256-token vocabulary (Llama 3) at temperature 1.5, top_p 0.95: the
+    # nucleus holds most of the vocabulary
+    sp = fwgpu.spec(256, 512, 2, 8, 2, 128256, 64, 500000.0, seed=128)
+    prompt = np.random.default_rng(128).integers(3, 128256, 6).astype(np.uint32)
+    with fwgpu.HostModel(synth=sp) as host, fw_cpu.OracleModel(host) as om:
+        exp = om.generate_sampled(prompt, 6, 1.5, 0.95, 1.0, 1234)
+        with fwgpu.GpuModel(host) as gm:
+            got = gm.generate(prompt, 6, 1.5, 0.95, 1.0, 1234)
+            again = gm.generate(prompt, 6, 1.5, 0.95, 1.0, 1234)
+    assert np.array_equal(got, exp), (got, exp)
+    assert np.array_equal(got, again)
