@@ -38,6 +38,11 @@ template <uint32_t T> struct Blk;
 template <> struct Blk<kQ4_0> { static constexpr int bytes = 18, pair_dw = 9; };
 template <> struct Blk<kQ5_0> { static constexpr int bytes = 22, pair_dw = 11; };
 template <> struct Blk<kQ8_0> { static constexpr int bytes = 34, pair_dw = 17; };
+// One 64-value quarter of a Q4_K super-block: its 8 code dwords, then the
+// super-block's 4 header dwords (d|dmin, 12 scale bytes).
+template <> struct Blk<kQ4_K> { static constexpr int bytes = 144, pair_dw = 12; };
+// One 56-byte quarter record of a repacked Q6_K super-block (14 dwords).
+template <> struct Blk<kQ6_KR> { static constexpr int bytes = 224, pair_dw = 14; };
 
 // fp16 bits (low half of h) -> fp32, exact incl. subnormals (v_cvt_f32_f16 with
 // fp16 denormals enabled, the gfx9 default).
@@ -145,6 +150,93 @@ __device__ __forceinline__ float dot_pair(const uint32_t *dw, const float *x, fl
         for (int k = 0; k < 8; k++) { q0[k] = align16(dw[k + 1], dw[k]); q1[k] = dw[9 + k]; }
         return dot_q8_0(h2f(dw[0]), q0, x) + dot_q8_0(h2f(dw[8] >> 16), q1, x + 32);
     }
+}
+
+// Σ over the two 32-value groups of a Q4_K quarter of (d·sc)·q·x − (dmin·m)·x
+// (quant.c:111-126, factored per group): q[8] = the quarter's 32 code bytes,
+// value i < 32 in the low nibble of byte i, value 32 + i in its high nibble.
+// ds/dm are the groups' rounded products d·sc and dmin·m; sx0/sx1 the sums of
+// x over the two groups.  Codes in 1/512 units from the fp8 conversion, as for Q4_0.
+__device__ __forceinline__ float dot_q4k_quarter(const uint32_t *q, const float *x, float ds0, float dm0, float ds1,
+                                                 float dm1, float sx0, float sx1)
+{
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+        const float2v l01 = nib2<false>(lo), l23 = nib2<true>(lo);
+        const float2v h01 = nib2<false>(hi), h23 = nib2<true>(hi);
+        a0 = __builtin_fmaf(l01.x, x[4 * i + 0], a0);
+        a1 = __builtin_fmaf(l01.y, x[4 * i + 1], a1);
+        a0 = __builtin_fmaf(l23.x, x[4 * i + 2], a0);
+        a1 = __builtin_fmaf(l23.y, x[4 * i + 3], a1);
+        b0 = __builtin_fmaf(h01.x, x[32 + 4 * i + 0], b0);
+        b1 = __builtin_fmaf(h01.y, x[32 + 4 * i + 1], b1);
+        b0 = __builtin_fmaf(h23.x, x[32 + 4 * i + 2], b0);
+        b1 = __builtin_fmaf(h23.y, x[32 + 4 * i + 3], b1);
+    }
+    const float s0 = (a0 + a1) * 512.0f, s1 = (b0 + b1) * 512.0f;
+    return __builtin_fmaf(ds0, s0, -dm0 * sx0) + __builtin_fmaf(ds1, s1, -dm1 * sx1);
+}
+
+// Q4_K quarter u (0..3) of a super-block whose header dwords are h[0..3]:
+// scales and mins of its groups 2u and 2u+1 (get_scale_min_k4, quant.c:66-85).
+// Groups j < 4 take bytes j and j+4 (6 low bits); groups 4 + j take the low
+// or high nibble of byte 8 + j and the top two bits of bytes j and 4 + j.  The
+// two groups of a quarter sit in adjacent bytes, so both come out of one
+// shift and mask, sc in the low two bytes of *sc, mins likewise.
+__device__ __forceinline__ void q4k_quarter_scales(const uint32_t *h, uint32_t u, uint32_t &sc, uint32_t &mn)
+{
+    const bool low = u < 2;
+    const uint32_t sh = (u & 1) * 16;
+    const uint32_t m1 = low ? 0x3F3Fu : 0x0F0Fu, m2 = low ? 0u : 0x3030u;
+    const uint32_t xs = low ? h[1] : h[3], xm = low ? h[2] : h[3], shm = low ? sh : sh + 4;
+    sc = ((xs >> sh) & m1) | ((h[1] >> (sh + 2)) & m2);
+    mn = ((xm >> shm) & m1) | ((h[2] >> (sh + 2)) & m2);
+}
+
+// Quarter u of a Q4_K super-block held as in Blk<kQ4_K> (codes dw[0..7], header dw[8..11]).
+__device__ __forceinline__ float dot_q4k_item(const uint32_t *dw, const float *x, float sx0, float sx1, uint32_t u)
+{
+    uint32_t sc, mn;
+    q4k_quarter_scales(dw + 8, u, sc, mn);
+    const float d = h2f(dw[8]), dmin = h2f(dw[8] >> 16);
+    return dot_q4k_quarter(dw, x, d * (float)(sc & 0xFFu), dmin * (float)(mn & 0xFFu), d * (float)(sc >> 8),
+                           dmin * (float)(mn >> 8), sx0, sx1);
+}
+
+// One quarter record of a repacked Q6_K super-block (14 dwords).  Values i of
+// the quarter (0..63) are q_i = lo4_i | hi2_i << 4 (quant.c:160-183):
+//   dw[k], k < 8:   byte b holds lo4 of value 4k+b (low nibble) and of value 32+4k+b (high);
+//   dw[8 + k/2]:    byte b holds hi2 of those two values, at bits 4-5 and 6-7 for even k,
+//                   at bits 0-1 and 2-3 for odd k;
+//   dw[12]:         the int8 scales of values 0-15, 16-31, 32-47, 48-63;
+//   dw[13]:         d (fp16) in the low half.
+// Result: Σ_g (d·sc_g)·(Σ_{i in g} q_i x_i − 32 Σ_{i in g} x_i), sx[g] the sums of x over the groups.
+__device__ __forceinline__ float dot_q6kr(const uint32_t *dw, const float *x, const float *sx)
+{
+    float a[4] = { 0.f, 0.f, 0.f, 0.f };
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t n = dw[k], h = dw[8 + k / 2];
+        const uint32_t hl = (k & 1) ? h << 4 : h, hh = (k & 1) ? h << 2 : h >> 2;
+        const uint32_t ql = (n & 0x0F0F0F0Fu) | (hl & 0x30303030u);
+        const uint32_t qh = ((n >> 4) & 0x0F0F0F0Fu) | (hh & 0x30303030u);
+        const int gl = k / 4, gh = 2 + k / 4;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            a[gl] = __builtin_fmaf((float)((ql >> (8 * b)) & 0xFFu), x[4 * k + b], a[gl]);
+            a[gh] = __builtin_fmaf((float)((qh >> (8 * b)) & 0xFFu), x[32 + 4 * k + b], a[gh]);
+        }
+    }
+    const float d = h2f(dw[13]);
+    float r = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float ds = d * (float)(int8_t)(dw[12] >> (8 * g));
+        r = __builtin_fmaf(ds, __builtin_fmaf(-32.0f, sx[g], a[g]), r);
+    }
+    return r;
 }
 
 // Load one pair of blocks (pair_dw dwords) from a dword-aligned address.

@@ -9,6 +9,10 @@ namespace fw {
 
 // ggml type ids on the path (gguf.c:155-174)
 enum : uint32_t { kF32 = 0, kQ4_0 = 2, kQ5_0 = 6, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
+// Q6_K rows re-laid out for the persistent step kernel (no ggml counterpart):
+// each 64-value quarter of a super-block as one 56-byte, 4-byte-aligned record,
+// 224 bytes per super-block (see repack_q6k).
+constexpr uint32_t kQ6_KR = 0x10e;
 
 // Device-resident step state read by every kernel of a token step, so one
 // captured graph serves every position.

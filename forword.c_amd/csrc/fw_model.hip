@@ -489,7 +489,10 @@ static int setup_mk(forword_gpu_t *h)
     uint32_t gs = 8;
     while (group % gs) gs >>= 1;
     const uint32_t units = c.n_head_kv * (group / gs);
-    if (!mk_supported(n, c.n_ff, hd, group, tl, h->out.type, h->embd.type) || units + 1 > 64) return 0;
+    // a Q6_K lm-head runs from a re-laid-out copy (whole super-blocks per row required)
+    const bool head_q6k = h->out.type == kQ6_K;
+    const uint32_t th = head_q6k ? kQ6_KR : h->out.type;
+    if (!mk_supported(n, c.n_ff, hd, group, tl, th, h->embd.type) || units + 1 > 64) return 0;
     int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 ||
@@ -503,6 +506,7 @@ static int setup_mk(forword_gpu_t *h)
     a.rb_embd = h->L[0].q.row_bytes;
     a.rb_ff = h->L[0].down.row_bytes;
     a.head_w = h->out.w; a.head_rb = h->out.row_bytes; a.out_norm = h->out_norm;
+    a.qa_lin = mk_q_align(tl); a.qa_head = mk_q_align(th);
     a.embd = h->embd.w; a.embd_type = h->embd.type; a.embd_row_bytes = h->embd.row_bytes; a.embd_scale = c.embd_scale;
     a.n_embd = n; a.n_ff = c.n_ff; a.n_head = c.n_head; a.n_kv = c.n_head_kv; a.head_dim = hd;
     a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
@@ -520,8 +524,8 @@ static int setup_mk(forword_gpu_t *h)
     if (ns > 256) ns = 256;
     if (ns < 1) ns = 1;
     a.n_splits = ns;
-    const size_t lds = mk_lds_bytes(a, (uint32_t)cus, tl, h->out.type);
-    const int wg = lds ? mk_max_workgroups(tl, h->out.type, lds) : 0;
+    const size_t lds = mk_lds_bytes(a, (uint32_t)cus, tl, th);
+    const int wg = lds ? mk_max_workgroups(tl, th, lds) : 0;
     if (wg != cus) {
         fprintf(stderr, "forword_gpu: persistent step kernel cannot launch (LDS %zu B); using per-phase kernels\n", lds);
         return 0;
@@ -541,6 +545,17 @@ static int setup_mk(forword_gpu_t *h)
         dalloc(h, (void **)&h->d_tatt, (size_t)n * 8, "tagged attention output") ||
         dalloc(h, (void **)&h->d_th, (size_t)c.n_ff * 8, "tagged ffn activations"))
         return -1;
+    if (head_q6k) {
+        const uint32_t n_sb = n / 256;
+        uint8_t *rp = nullptr;
+        if (dalloc(h, (void **)&rp, (size_t)c.n_vocab * n_sb * 224, "lm-head Q6_K records")) return -1;
+        if (launch_repack_q6k(h->out.w, h->out.row_bytes, c.n_vocab, n_sb, rp, h->stream) != hipSuccess) {
+            set_err("persistent step kernel: lm-head repack launch failed");
+            return -1;
+        }
+        a.head_w = rp;
+        a.head_rb = (uint64_t)n_sb * 224;
+    }
     a.tx = h->d_tx; a.tatt = h->d_tatt; a.th = h->d_th;
     if (hipMemcpy(h->d_layers, layers.data(), layers.size() * sizeof(MkLayer), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(h->d_bar, 0, (size_t)wg * 128) != hipSuccess || hipMemset(h->d_mk_tickets, 0, 64 * 4) != hipSuccess ||
@@ -563,7 +578,7 @@ static int setup_mk(forword_gpu_t *h)
         a.prof = h->d_prof;
     }
     h->mk_tl = tl;
-    h->mk_th = h->out.type;
+    h->mk_th = th;
     h->mk_wg = (uint32_t)wg;
     h->mk_lds = lds;
     h->mk_epoch = 0;

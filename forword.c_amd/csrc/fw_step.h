@@ -17,7 +17,7 @@ struct MkGemv {
     uint32_t n_rows;         // rows of the phase (QKV: sum; FFN: rows of one matrix)
     uint32_t n_cols;
     uint64_t row_bytes;
-    uint32_t type;
+    uint32_t qa;             // slice alignment of the phase's weight type (pairs per slice a multiple of it)
 };
 
 enum MkKind : uint32_t { MK_QKV = 0, MK_ATTN = 1, MK_WO = 2, MK_FFN = 3, MK_DOWN = 4, MK_HEAD = 5 };
@@ -67,6 +67,7 @@ struct MkArgs {
     uint32_t *am_i;
     uint64_t *prof;          // optional: wall-clock stamp at kernel start, then after every phase
     uint32_t epoch0, n_steps;
+    uint32_t qa_lin, qa_head;  // slice alignment of the layer linears' and the lm-head's weight types
 };
 
 // Threads of one workgroup, and how many of them poll barrier flags and load
@@ -77,7 +78,8 @@ constexpr uint32_t kMkPollers = 256;
 // Barriers one token step performs (the host advances its epoch by this much).
 inline uint32_t mk_barriers_per_step(uint32_t n_layer) { return 5 * n_layer + 1; }
 // Whether the persistent kernel supports this model (else the per-kernel path
-// runs): every layer linear of one type, Q4_0/Q5_0/Q8_0 linears and lm-head.
+// runs): every layer linear of one type, Q4_0/Q5_0/Q8_0/Q4_K linears; lm-head
+// of those types or kQ6_KR (a Q6_K head after launch_repack_q6k).
 bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
                   uint32_t head_type, uint32_t embd_type);
 // Dynamic LDS of one workgroup (args fully set up, n_splits included), 0 if
@@ -85,6 +87,12 @@ bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t gr
 size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type);
 // Workgroups of one cooperative launch (one per CU), 0 if it cannot launch.
 int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes);
+// Q6_K matrix [n_rows][n_sb super-blocks] (rows src_rb bytes apart) into
+// kQ6_KR records at dst (n_rows * n_sb * 224 bytes, 4-byte aligned).
+hipError_t launch_repack_q6k(const uint8_t *src, uint64_t src_rb, uint32_t n_rows, uint32_t n_sb, uint8_t *dst,
+                             hipStream_t s);
+// Slice alignment of a weight type in the persistent kernel (MkArgs::qa_lin, qa_head).
+uint32_t mk_q_align(uint32_t type);
 hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,
                      hipStream_t s);
 

@@ -217,12 +217,18 @@ __host__ __device__ inline uint32_t mk_rows_per_wg(uint32_t n_rows, uint32_t n_w
 }
 
 // Block pairs per column slice: the pairs of a row spread evenly over the
-// waves (at most 64 per slice).
-__host__ __device__ inline uint32_t slice_pairs(uint32_t n_pairs)
+// waves (at most 64 per slice), rounded up to a multiple of qa.  Q4_K slices
+// hold whole super-blocks (qa = 4 quarters): the four lanes of a lane quad then
+// share one super-block, whose header they fetch a dword each.
+__host__ __device__ inline uint32_t slice_pairs(uint32_t n_pairs, uint32_t qa)
 {
-    const uint32_t q = (n_pairs + MK_WAVES - 1) / MK_WAVES;
-    return q < 1 ? 1 : q > 64 ? 64 : q;
+    uint32_t q = (n_pairs + MK_WAVES - 1) / MK_WAVES;
+    q = q < 1 ? 1 : q > 64 ? 64 : q;
+    return (q + qa - 1) / qa * qa;
 }
+
+// Slice alignment of a weight type (see slice_pairs).
+__host__ __device__ constexpr uint32_t q_align(uint32_t t) { return t == kQ4_K ? 4u : 1u; }
 
 // Lanes per row group: the power of two that holds a slice's pairs.
 __host__ __device__ inline uint32_t lanes_per_row(uint32_t q)
@@ -233,9 +239,9 @@ __host__ __device__ inline uint32_t lanes_per_row(uint32_t q)
 }
 
 // Column slices of a row of n_cols values.
-__host__ __device__ inline uint32_t n_slices(uint32_t n_cols)
+__host__ __device__ inline uint32_t n_slices(uint32_t n_cols, uint32_t qa)
 {
-    const uint32_t np = n_cols / 64, q = slice_pairs(np);
+    const uint32_t np = n_cols / 64, q = slice_pairs(np, qa);
     return (np + q - 1) / q;
 }
 
@@ -250,14 +256,14 @@ struct Map {
 
 // Fewer slices than waves: several waves share a slice and split its row
 // groups.  More slices than waves: each wave walks slices wave, wave + 4, ...
-__device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols)
+__device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols, uint32_t qa)
 {
     Map m;
     const uint32_t per = mk_rows_per_wg(n_rows, gridDim.x);
     m.lo = min(n_rows, blockIdx.x * per);
     m.hi = min(n_rows, m.lo + per);
     m.n_pairs = n_cols / 64;
-    m.Q = slice_pairs(m.n_pairs);
+    m.Q = slice_pairs(m.n_pairs, qa);
     m.P = lanes_per_row(m.Q);
     m.S = (m.n_pairs + m.Q - 1) / m.Q;
     const uint32_t wave = wave_id(), lane = tid() & 63;
@@ -314,15 +320,21 @@ __device__ __forceinline__ const uint8_t *row_ptr(const MkGemv &g, uint32_t r, i
 // explicit.  The first items of the next phase are issued right after a
 // workgroup arrives at a barrier and land during the barrier and the staging.
 //
-// A block pair is moved in 16-byte pieces and a tail (Q4_0 36 = 16+16+4,
-// Q5_0 44 = 16+16+12, Q8_0 68 = 4*16+4).  A piece of s bytes puts lane l's
-// bytes at l*s in LDS for s = 4 and 16 and at l*16 for s = 12, so a pair takes
-// 64 * (16 * n16 + 16 or 4) bytes of its slot.
+// A lane's share of an item (a block pair, a Q4_K quarter or a repacked Q6_K
+// quarter record) is moved in 16-byte pieces and one or two tails: Q4_0 36 =
+// 16+16+4, Q5_0 44 = 16+16+12, Q8_0 68 = 4*16+4; Q4_K the quarter's 32 code
+// bytes (16+16) and one dword of its super-block's header (the lane quad
+// fetches the four); Q6_K records 56 = 16+16+12+12.  A piece of s bytes puts
+// lane l's bytes at l*s in LDS for s = 4 and 16 and at l*16 for s = 12.
 
 __host__ __device__ constexpr uint32_t dma_n16(uint32_t t) { return t == kQ8_0 ? 4u : 2u; }
-__host__ __device__ constexpr uint32_t dma_tail(uint32_t t) { return t == kQ5_0 ? 12u : 4u; }
-__host__ __device__ constexpr uint32_t dma_count(uint32_t t) { return dma_n16(t) + 1u; }
-__host__ __device__ constexpr uint32_t dma_pair_lds(uint32_t t) { return 64u * (16u * dma_n16(t) + (dma_tail(t) == 4u ? 4u : 16u)); }
+__host__ __device__ constexpr uint32_t dma_tail(uint32_t t) { return t == kQ5_0 || t == kQ6_KR ? 12u : 4u; }
+__host__ __device__ constexpr uint32_t dma_tail2(uint32_t t) { return t == kQ6_KR ? 12u : 0u; }
+__host__ __device__ constexpr uint32_t dma_count(uint32_t t) { return dma_n16(t) + 1u + (dma_tail2(t) ? 1u : 0u); }
+__host__ __device__ constexpr uint32_t dma_pair_lds(uint32_t t)
+{
+    return 64u * (16u * dma_n16(t) + (dma_tail(t) == 4u ? 4u : 16u) + (dma_tail2(t) ? 16u : 0u));
+}
 __host__ __device__ constexpr uint32_t slot_bytes(uint32_t t, uint32_t M) { return M * dma_pair_lds(t); }
 
 constexpr uint32_t MK_NS_MAX = 12;          // ring slots per wave at most
@@ -404,13 +416,29 @@ __device__ __forceinline__ void dma_lds(const FW_GLOBAL uint8_t *src, uint8_t *l
 }
 #undef FW_DMA_LDS
 
+// Lane's share of pair `pair` of a row into an item slot at dst.
 template <uint32_t T>
-__device__ __forceinline__ void dma_pair(const uint8_t *src, uint8_t *dst)
+__device__ __forceinline__ void dma_pair(const uint8_t *row, uint32_t pair, uint8_t *dst)
 {
-    const FW_GLOBAL uint8_t *s = gptr(src);
+    if constexpr (T == kQ4_K) {
+        // quarter pair & 3 of super-block pair / 4: codes at 16 + 32 * quarter, and
+        // header dword (lane & 3): the quad's lanes hold one super-block's quarters
+        const FW_GLOBAL uint8_t *sb = gptr(row) + (size_t)(pair >> 2) * 144;
+        dma_lds<16>(sb + 16 + 32 * (pair & 3), dst);
+        dma_lds<16>(sb + 32 + 32 * (pair & 3), dst + 1024);
+        dma_lds<4>(sb + 4 * (tid() & 3), dst + 2048);
+    } else if constexpr (T == kQ6_KR) {
+        const FW_GLOBAL uint8_t *s = gptr(row) + (size_t)pair * 56;
+        dma_lds<16>(s, dst);
+        dma_lds<16>(s + 16, dst + 1024);
+        dma_lds<12>(s + 32, dst + 2048);
+        dma_lds<12>(s + 44, dst + 3072);
+    } else {
+        const FW_GLOBAL uint8_t *s = gptr(row) + (size_t)pair * (2 * Blk<T>::bytes);
 #pragma unroll
-    for (uint32_t i = 0; i < dma_n16(T); i++) dma_lds<16>(s + 16 * i, dst + 1024 * i);
-    dma_lds<(int)dma_tail(T)>(s + 16 * dma_n16(T), dst + 1024 * dma_n16(T));
+        for (uint32_t i = 0; i < dma_n16(T); i++) dma_lds<16>(s + 16 * i, dst + 1024 * i);
+        dma_lds<(int)dma_tail(T)>(s + 16 * dma_n16(T), dst + 1024 * dma_n16(T));
+    }
 }
 
 // Issue item c.  Every load is issued: a row past the workgroup's last one and
@@ -425,7 +453,7 @@ __device__ __forceinline__ void dma_item(const MkGemv &g, const Map &m, const Cu
     uint8_t *slot = ring + c.slot * slot_bytes(T, M);
 #pragma unroll
     for (int mat = 0; mat < M; mat++)
-        dma_pair<T>(row_ptr<M>(g, r, mat) + (size_t)pair * (2 * Blk<T>::bytes), slot + mat * dma_pair_lds(T));
+        dma_pair<T>(row_ptr<M>(g, r, mat), pair, slot + mat * dma_pair_lds(T));
 }
 
 template <uint32_t T, int M>
@@ -441,11 +469,19 @@ __device__ __forceinline__ void read_item(const uint8_t *slot, uint32_t (&dw)[M]
             dw[mat][4 * i] = v.x; dw[mat][4 * i + 1] = v.y; dw[mat][4 * i + 2] = v.z; dw[mat][4 * i + 3] = v.w;
         }
         const uint8_t *t = p + 1024 * dma_n16(T);
-        if constexpr (dma_tail(T) == 4) {
+        if constexpr (T == kQ4_K) {
+            // the quad's four header dwords, side by side
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(t + 16 * (lane >> 2));
+            dw[mat][8] = v.x; dw[mat][9] = v.y; dw[mat][10] = v.z; dw[mat][11] = v.w;
+        } else if constexpr (dma_tail(T) == 4) {
             dw[mat][4 * dma_n16(T)] = *reinterpret_cast<const uint32_t *>(t + 4 * lane);
         } else {
             const u32x4 v = *reinterpret_cast<const u32x4 *>(t + 16 * lane);
             dw[mat][8] = v.x; dw[mat][9] = v.y; dw[mat][10] = v.z;
+            if constexpr (dma_tail2(T) != 0) {
+                const u32x4 w = *reinterpret_cast<const u32x4 *>(t + 1024 + 16 * lane);
+                dw[mat][11] = w.x; dw[mat][12] = w.y; dw[mat][13] = w.z;
+            }
         }
     }
 }
@@ -470,13 +506,13 @@ __device__ __forceinline__ void wait_items(uint32_t k)
 }
 
 // The 64 input values of the lane's pair in slice sl (zero past the row) and,
-// for the offset formats, their two block sums.
+// for the offset formats, their sums over the blocks (Q4_0, Q5_0) or scale
+// groups (Q4_K: two of 32 values; Q6_K: four of 16).
 template <uint32_t T>
-__device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t sl, float (&xv)[64], float &sx0,
-                                       float &sx1)
+__device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t sl, float (&xv)[64], float (&sx)[4])
 {
     const uint32_t pair = sl * m.Q + m.ps;
-    sx0 = sx1 = 0.f;
+    sx[0] = sx[1] = sx[2] = sx[3] = 0.f;
     if (m.ps < m.Q && pair < m.n_pairs) {
         // Read through inline asm: for compiler-visible LDS reads the compiler
         // cannot tell xs from the weight rings and first waits for every DMA
@@ -499,12 +535,20 @@ __device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t s
         for (int i = 0; i < 16; i++) {
             xv[4 * i] = r[i][0]; xv[4 * i + 1] = r[i][1]; xv[4 * i + 2] = r[i][2]; xv[4 * i + 3] = r[i][3];
         }
-        if constexpr (T != kQ8_0) {
+        if constexpr (T == kQ6_KR) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) { s0 += xv[16 * g + i]; s1 += xv[16 * g + i + 1]; }
+                sx[g] = s0 + s1;
+            }
+        } else if constexpr (T != kQ8_0) {
             float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
             for (int i = 0; i < 32; i += 2) { s0 += xv[i]; s1 += xv[i + 1]; s2 += xv[32 + i]; s3 += xv[33 + i]; }
-            sx0 = s0 + s1;
-            sx1 = s2 + s3;
+            sx[0] = s0 + s1;
+            sx[1] = s2 + s3;
         }
     } else {
 #pragma unroll
@@ -517,7 +561,7 @@ __device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t s
 template <uint32_t T, int M>
 __device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint32_t fixed, uint32_t attn_bytes)
 {
-    const Map m = plan(g.n_rows, g.n_cols);
+    const Map m = plan(g.n_rows, g.n_cols, g.qa);
     const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
     const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
     const uint32_t n = min(min(rg.ns, MK_PF), n_sl * m.n_my);
@@ -527,6 +571,15 @@ __device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint
         advance(c, m.n_my, rg.ns);
     }
     return n;
+}
+
+// Dot of one item's dwords with the lane's 64 input values.
+template <uint32_t T>
+__device__ __forceinline__ float item_dot(const uint32_t *dw, const float (&xv)[64], const float (&sx)[4], uint32_t q)
+{
+    if constexpr (T == kQ4_K) return dot_q4k_item(dw, xv, sx[0], sx[1], q);
+    else if constexpr (T == kQ6_KR) return dot_q6kr(dw, xv, sx);
+    else return dot_pair<T>(dw, xv, sx[0], sx[1]);
 }
 
 template <int CTRL>
@@ -577,7 +630,7 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
                                      uint32_t attn_bytes, uint32_t n_pre)
 {
     constexpr int D = (int)dma_count(T) * M, NDW = Blk<T>::pair_dw;
-    const Map m = plan(g.n_rows, g.n_cols);
+    const Map m = plan(g.n_rows, g.n_cols, g.qa);
     const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
     const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
     const uint32_t n_items = n_sl * m.n_my;
@@ -588,10 +641,11 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
         advance(is, m.n_my, rg.ns);
     }
     uint32_t it = 0, slot = 0;
+    const uint32_t lane_q = tid() & 3;                           // Q4_K: the lane's quarter of its super-block
     for (uint32_t si = 0; si < n_sl; si++) {
         const uint32_t sl = m.slice + si * m.sstep;
-        float xv[64], sx0, sx1;
-        load_x<T>(xs, m, sl, xv, sx0, sx1);
+        float xv[64], sx[4];
+        load_x<T>(xs, m, sl, xv, sx);
         const bool pair_on = m.ps < m.Q && sl * m.Q + m.ps < m.n_pairs;
         for (uint32_t k = 0; k < m.n_my; k++, it++) {
             wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
@@ -608,7 +662,7 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
             float acc[M];
 #pragma unroll
             for (int mat = 0; mat < M; mat++) {
-                acc[mat] = dot_pair<T>(dw[mat], xv, sx0, sx1);
+                acc[mat] = item_dot<T>(dw[mat], xv, sx, lane_q);
                 if (!on) acc[mat] = 0.f;
             }
             lane_sum<M>(acc, m.P);
@@ -645,7 +699,7 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols), hd = a.head_dim, half = hd / 2;
+    const uint32_t ns = n_slices(g.n_cols, g.qa), hd = a.head_dim, half = hd / 2;
     const uint32_t kvd = a.n_kv * hd, nq = g.rows[0];
     for (uint32_t rl = 2 * tid(); rl < hi - lo; rl += 2 * MK_THREADS) {
         const uint32_t r = lo + rl;
@@ -678,7 +732,7 @@ __device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, cons
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols);
+    const uint32_t ns = n_slices(g.n_cols, g.qa);
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const uint32_t r = lo + rl;
         const float v = x_own[rl] + row_sum<1>(part, rl, 0, ns);
@@ -703,7 +757,7 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols);
+    const uint32_t ns = n_slices(g.n_cols, g.qa);
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const float gv = row_sum<2>(part, rl, 0, ns);
         const float av = a.act == ACT_SILU ? silu_f(gv) : a.act == ACT_GELU ? gelu_erf(gv) : gelu_tanh(gv);
@@ -748,7 +802,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
     __shared__ uint32_t s_last;
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols);
+    const uint32_t ns = n_slices(g.n_cols, g.qa);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
@@ -1056,11 +1110,12 @@ struct MkLds {
 __host__ __device__ inline uint32_t mk_fixed_floats(const MkArgs &a, uint32_t n_wg, uint32_t &part)
 {
     const uint32_t kvd = a.n_kv * a.head_dim;
-    part = mk_rows_per_wg(a.n_vocab, n_wg) * n_slices(a.n_embd);                       // lm-head
-    const uint32_t c[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg) * n_slices(a.n_embd),   // QKV
-                           mk_rows_per_wg(a.n_ff, n_wg) * 2 * n_slices(a.n_embd),           // gate, up
-                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_embd),             // WO
-                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff) };             // down
+    const uint32_t ql = a.qa_lin;
+    part = mk_rows_per_wg(a.n_vocab, n_wg) * n_slices(a.n_embd, a.qa_head);                   // lm-head
+    const uint32_t c[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg) * n_slices(a.n_embd, ql),   // QKV
+                           mk_rows_per_wg(a.n_ff, n_wg) * 2 * n_slices(a.n_embd, ql),           // gate, up
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_embd, ql),             // WO
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff, ql) };             // down
     for (uint32_t v : c) part = v > part ? v : part;
     part = (part + 3) & ~3u;
     return part + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4) + mk_rows_per_wg(a.n_embd, n_wg) + a.head_dim;
@@ -1103,7 +1158,9 @@ __device__ __forceinline__ MkGemv phase_gemv(const MkArgs &a, const MkLayer *tab
     MkGemv g{};
     g.n_cols = a.n_embd;
     g.row_bytes = a.rb_embd;
+    g.qa = a.qa_lin;
     if (kind == MK_HEAD) {
+        g.qa = a.qa_head;
         g.w[0] = a.head_w;
         g.rows[0] = g.n_rows = a.n_vocab;
         g.row_bytes = a.head_rb;
@@ -1143,11 +1200,11 @@ __device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, 
     uint32_t lo, hi;
     wg_rows(a.n_embd, lo, hi);
     const uint8_t *row = a.embd + (size_t)tok * a.embd_row_bytes;
-    const uint32_t bb = block_bytes_dev(a.embd_type);
+    const uint32_t bb = block_bytes_dev(a.embd_type), bv = block_values_dev(a.embd_type);
     float ss = 0.f;
     for (uint32_t j = tid(); j < a.n_embd; j += MK_THREADS) {
         float v = a.embd_type == kF32 ? reinterpret_cast<const float *>(row)[j]
-                                      : dequant_one(row + (size_t)(j / 32) * bb, a.embd_type, j & 31);
+                                      : dequant_one(row + (size_t)(j / bv) * bb, a.embd_type, j % bv);
         if (a.embd_scale != 1.0f) v *= a.embd_scale;
         xs[swz(j)] = v;
         ss = __builtin_fmaf(v, v, ss);
@@ -1257,9 +1314,60 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
     }
 }
 
+// Q6_K rows into the persistent kernel's quarter records (one thread per
+// record).  A Q6_K super-block is 210 bytes, so every other one starts at an
+// odd halfword and cannot be moved by dword DMA; the records hold the same
+// bits (quant.c:160-183), 4-byte aligned.  Quarter u of a super-block is its
+// values 64u..64u+63: h = u / 2, kk = 2 (u & 1) for the first 32 values and
+// kk + 1 for the next 32, l = the value's index within its 32.
+__global__ __launch_bounds__(256) void k_repack_q6k(const uint8_t *src, uint64_t src_rb, uint32_t n_rows, uint32_t n_sb,
+                                                    uint32_t *dst)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n_rows * n_sb * 4) return;
+    const uint32_t u = (uint32_t)(i & 3);
+    const uint64_t sbi = i >> 2;
+    const uint8_t *blk = src + (sbi / n_sb) * src_rb + (sbi % n_sb) * 210;
+    const uint32_t h = u >> 1, k0 = 2 * (u & 1);
+    uint32_t w[14];
+#pragma unroll
+    for (int k = 0; k < 14; k++) w[k] = 0;
+    for (uint32_t l = 0; l < 32; l++) {
+        uint32_t lo[2], hb[2];
+        for (uint32_t e = 0; e < 2; e++) {
+            const uint32_t kk = k0 + e;
+            const uint32_t ql = blk[h * 64 + l + 32 * (kk & 1)];
+            lo[e] = kk >= 2 ? ql >> 4 : ql & 15u;
+            hb[e] = ((uint32_t)blk[128 + h * 32 + l] >> (2 * kk)) & 3u;
+        }
+        const uint32_t k = l / 4, b = 8 * (l % 4), sh = (k & 1) ? 0u : 4u;
+        w[k] |= (lo[0] | lo[1] << 4) << b;
+        w[8 + k / 2] |= (hb[0] << sh | hb[1] << (sh + 2)) << b;
+    }
+    const uint8_t *sc = blk + 192 + 4 * u;
+    w[12] = (uint32_t)sc[0] | (uint32_t)sc[1] << 8 | (uint32_t)sc[2] << 16 | (uint32_t)sc[3] << 24;
+    w[13] = (uint32_t)blk[208] | (uint32_t)blk[209] << 8;
+    uint32_t *o = dst + (size_t)i * 14;
+#pragma unroll
+    for (int k = 0; k < 14; k++) o[k] = w[k];
+}
+
+hipError_t launch_repack_q6k(const uint8_t *src, uint64_t src_rb, uint32_t n_rows, uint32_t n_sb, uint8_t *dst,
+                             hipStream_t s)
+{
+    const uint64_t n = (uint64_t)n_rows * n_sb * 4;
+    if (n == 0) return hipSuccess;
+    if (((uintptr_t)dst & 3) || (n + 255) / 256 > 0x7fffffffu) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_repack_q6k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, src_rb, n_rows, n_sb,
+                       reinterpret_cast<uint32_t *>(dst));
+    return hipGetLastError();
+}
+
 // ── host side ───────────────────────────────────────────────────────────────
 
-static bool mk_type_ok(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
+static bool mk_kernel_exists(uint32_t tl, uint32_t th);
+
+static bool mk_small_type(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
 
 bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
                   uint32_t head_type, uint32_t embd_type)
@@ -1267,7 +1375,10 @@ bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t gr
     if (n_embd % 64 || n_ff % 64 || n_embd / 64 > 64 * MK_SMAX || n_ff / 64 > 64 * MK_SMAX) return false;
     if (head_dim != 32 && head_dim != 64 && head_dim != 128) return false;
     if (group < 1) return false;                    // any group, in units of mk_attn_gs query heads
-    return mk_type_ok(linear_type) && mk_type_ok(head_type) && (mk_type_ok(embd_type) || embd_type == kF32);
+    const bool lin_ok = mk_small_type(linear_type) || (linear_type == kQ4_K && n_embd % 256 == 0 && n_ff % 256 == 0);
+    const bool head_ok = mk_small_type(head_type) || ((head_type == kQ4_K || head_type == kQ6_KR) && n_embd % 256 == 0);
+    const bool embd_ok = mk_small_type(embd_type) || embd_type == kF32 || embd_type == kQ4_K || embd_type == kQ6_K;
+    return lin_ok && head_ok && embd_ok && mk_kernel_exists(linear_type, head_type);
 }
 
 size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type)
@@ -1287,15 +1398,23 @@ size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32
 
 typedef void (*mk_kernel_t)(MkArgs);
 
+// Instantiated (linear, lm-head) type pairs: the Q4_0/Q5_0/Q8_0 files' pairs,
+// those with a Q6_K head (its repacked form), and Q4_K layers with a Q4_K,
+// Q6_K or Q8_0 head.
 static mk_kernel_t mk_kernel(uint32_t tl, uint32_t th)
 {
 #define K(A, B) if (tl == A && th == B) return k_decode<A, B>;
-    K(kQ4_0, kQ4_0) K(kQ4_0, kQ5_0) K(kQ4_0, kQ8_0)
-    K(kQ5_0, kQ4_0) K(kQ5_0, kQ5_0) K(kQ5_0, kQ8_0)
-    K(kQ8_0, kQ4_0) K(kQ8_0, kQ5_0) K(kQ8_0, kQ8_0)
+    K(kQ4_0, kQ4_0) K(kQ4_0, kQ5_0) K(kQ4_0, kQ8_0) K(kQ4_0, kQ6_KR)
+    K(kQ5_0, kQ4_0) K(kQ5_0, kQ5_0) K(kQ5_0, kQ8_0) K(kQ5_0, kQ6_KR)
+    K(kQ8_0, kQ4_0) K(kQ8_0, kQ5_0) K(kQ8_0, kQ8_0) K(kQ8_0, kQ6_KR)
+    K(kQ4_K, kQ4_K) K(kQ4_K, kQ6_KR) K(kQ4_K, kQ8_0)
 #undef K
     return nullptr;
 }
+
+static bool mk_kernel_exists(uint32_t tl, uint32_t th) { return mk_kernel(tl, th) != nullptr; }
+
+uint32_t mk_q_align(uint32_t type) { return q_align(type); }
 
 int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes)
 {

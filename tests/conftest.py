@@ -75,3 +75,19 @@ def check_logit_stats(lg, row, f, atol=2e-3, rtol=1e-3, strict=True):
     sum_tol = lg.size * atol + rtol * float(np.abs(lg.astype(np.float64)).sum())
     got_sum = float(np.sum(lg, dtype=np.float64))
     assert abs(got_sum - row[4]) <= sum_tol, f"logit sum at forward {f}: {got_sum} vs {row[4]}"
+
+
+class kernel_choice:
+    """FORWORD_GPU_MEGAKERNEL=0 selects the per-phase kernels for handles
+    opened inside the block; otherwise the persistent step kernel runs where
+    the model allows it."""
+
+    def __init__(self, persistent):
+        self.persistent = persistent
+
+    def __enter__(self):
+        if not self.persistent:
+            os.environ["FORWORD_GPU_MEGAKERNEL"] = "0"
+
+    def __exit__(self, *a):
+        os.environ.pop("FORWORD_GPU_MEGAKERNEL", None)

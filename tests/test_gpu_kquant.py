@@ -3,13 +3,15 @@ bit-exact to the reference's decoders (golden fixtures written by the compiled
 reference), quant_matvec within tolerance of the reference's outputs
 (quant_matvec.c:231-261), and a Q4_K/Q6_K model equal to the oracle: logits
 within max-abs 2e-3 / rel 1e-3, identical greedy tokens, and the batched
-prefill on the same model."""
+prefill on the same model, on the persistent step kernel (Q4_K linears in
+place, a Q6_K lm-head from its re-laid-out copy) and on the per-phase kernels."""
 import numpy as np
 import pytest
 
 import fw_cpu
 import fwgpu
 import golden_specs as gs
+from conftest import kernel_choice
 from fwgpu import DeviceBuffer as DB, ops
 
 pytestmark = pytest.mark.gpu
@@ -67,17 +69,34 @@ def test_quant_matvec_vs_reference(case, gold_kquant):
     assert np.all(err <= 2e-5 * bound + 1e-30), f"max err/bound {np.max(err / (bound + 1e-30))}"
 
 
-def kq_spec():
-    # Q4_K linears and embedding, Q6_K output (the Q4_K_M layout's two types)
-    return fwgpu.spec(512, 1024, 2, 8, 2, 2000, 96, 10000.0, linear_type=gs.Q4K, embd_type=gs.Q4K,
-                      output_type=gs.Q6K, seed=1212)
+def kq_spec(name="q4k"):
+    """Q4_K linears and embedding with a Q6_K output (the Q4_K_M layout's two
+    types); the same layers with a Q8_0 output; Q4_0 layers with a Q6_K output
+    (llama.cpp's Q4_0 files keep the output Q6_K).  "q4k_odd": column slices
+    padded to whole super-blocks (768 = 3 x 256 columns, n_ff 1280 = 5 x 256)."""
+    if name == "q4k":
+        return fwgpu.spec(512, 1024, 2, 8, 2, 2000, 96, 10000.0, linear_type=gs.Q4K, embd_type=gs.Q4K,
+                          output_type=gs.Q6K, seed=1212)
+    if name == "q4k_q8":
+        return fwgpu.spec(512, 1024, 2, 8, 2, 2000, 96, 10000.0, linear_type=gs.Q4K, embd_type=gs.Q4K,
+                          output_type=fwgpu.GGML_Q8_0, seed=1214)
+    if name == "q4_0_q6k":
+        return fwgpu.spec(512, 1024, 2, 8, 2, 2000, 96, 10000.0, linear_type=fwgpu.GGML_Q4_0,
+                          embd_type=fwgpu.GGML_Q4_0, output_type=gs.Q6K, seed=1215)
+    assert name == "q4k_odd"
+    return fwgpu.spec(768, 1280, 2, 12, 4, 1500, 96, 10000.0, linear_type=gs.Q4K, embd_type=gs.Q6K,
+                      output_type=gs.Q6K, seed=1216)
 
 
-def test_kquant_model_matches_oracle():
-    prompt = np.random.default_rng(12).integers(3, 2000, 10).astype(np.uint32)
-    with fwgpu.HostModel(synth=kq_spec()) as host, fw_cpu.OracleModel(host) as om:
-        with fwgpu.GpuModel(host) as gm:
-            assert not gm.persistent                     # K-quants run the per-phase kernels
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_phase"])
+@pytest.mark.parametrize("name", ["q4k", "q4k_q8", "q4_0_q6k", "q4k_odd"])
+def test_kquant_model_matches_oracle(name, persistent):
+    """Per-token decode, the device-resident greedy loop and the batched prefill
+    against the oracle, on the persistent step kernel and on the per-phase kernels."""
+    prompt = np.random.default_rng(12).integers(3, 1500, 10).astype(np.uint32)
+    with fwgpu.HostModel(synth=kq_spec(name)) as host, fw_cpu.OracleModel(host) as om:
+        with kernel_choice(persistent), fwgpu.GpuModel(host) as gm:
+            assert gm.persistent == persistent
             toks = list(prompt)
             for f in range(len(prompt) + 5):
                 exp = om.forward(int(toks[f]), f)
@@ -86,10 +105,11 @@ def test_kquant_model_matches_oracle():
                 assert fw_cpu.argmax(got) == fw_cpu.argmax(exp)
                 if f + 1 >= len(toks):
                     toks.append(fw_cpu.argmax(exp))
+            check_close(gm.layer_trace().reshape(-1), om.trace().reshape(-1), "residual stream")
             ref_gen = np.array(toks[len(prompt):len(prompt) + 6], np.uint32)
-        with fwgpu.GpuModel(host) as gm:
+        with kernel_choice(persistent), fwgpu.GpuModel(host) as gm:
             assert np.array_equal(gm.generate_greedy(prompt, 6), ref_gen)
-        with fwgpu.GpuModel(host) as gm:
+        with kernel_choice(persistent), fwgpu.GpuModel(host) as gm:
             lg = gm.prefill(prompt)
             assert fw_cpu.argmax(lg) == int(ref_gen[0])
             assert np.array_equal(gm.generate_greedy_batched(prompt, 6), ref_gen)

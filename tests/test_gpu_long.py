@@ -16,6 +16,7 @@ import pytest
 
 import fw_cpu
 import fwgpu
+from conftest import kernel_choice
 
 pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-3, 1e-3
@@ -26,20 +27,6 @@ def close(got, exp, what):
     bad = err > ATOL + RTOL * np.abs(exp)
     assert not bad.any(), f"{what}: {bad.sum()} elements out of tolerance, max err {err.max():.3g}"
     return float(err.max())
-
-
-class kernel_choice:
-    """FORWORD_GPU_MEGAKERNEL=0 selects the per-phase kernels for new handles."""
-
-    def __init__(self, persistent):
-        self.persistent = persistent
-
-    def __enter__(self):
-        if not self.persistent:
-            os.environ["FORWORD_GPU_MEGAKERNEL"] = "0"
-
-    def __exit__(self, *a):
-        os.environ.pop("FORWORD_GPU_MEGAKERNEL", None)
 
 
 def say(msg):

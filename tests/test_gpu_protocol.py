@@ -14,24 +14,10 @@ import numpy as np
 import pytest
 
 import fwgpu
-from conftest import check_logit_stats
+from conftest import check_logit_stats, kernel_choice
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-
-
-class kernel_choice:
-    """FORWORD_GPU_MEGAKERNEL=0 selects the per-phase kernels for new handles."""
-
-    def __init__(self, persistent):
-        self.persistent = persistent
-
-    def __enter__(self):
-        if not self.persistent:
-            os.environ["FORWORD_GPU_MEGAKERNEL"] = "0"
-
-    def __exit__(self, *a):
-        os.environ.pop("FORWORD_GPU_MEGAKERNEL", None)
 
 
 def load_protocol():
