@@ -108,12 +108,15 @@ class Hip:
         return g, ex
 
 
-def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34):
+def step_bytes(cfg, pos, linear_bb=18, embd_bb=34, out_bb=34, mix_bb=None):
     """Algorithmic bytes of one token step at position pos: weights, embedding row, norm
-    weights, KV read (rows 0..pos incl. the one just written) and KV write."""
+    weights, KV read (rows 0..pos incl. the one just written) and KV write.  mix_bb:
+    bytes per 32 values of attn_v and ffn_down in the even layers (Q4_K_M layout)."""
     n, ff, L, hd, kv = cfg.n_embd, cfg.n_ff, cfg.n_layer, cfg.head_dim, cfg.n_head_kv
     n_in = 2 if cfg.use_ffn_gate else 1                 # gate and up, or up alone
     lin = L * ((n // 32) * linear_bb * (2 * n + 2 * kv * hd + n_in * ff) + (ff // 32) * linear_bb * n)
+    if mix_bb is not None:
+        lin += ((L + 1) // 2) * (mix_bb - linear_bb) * ((n // 32) * kv * hd + (ff // 32) * n)
     head = (n // 32) * out_bb * cfg.n_vocab
     embd = (n // 32) * embd_bb
     norms = 4 * n * (2 * L + 1)
@@ -286,7 +289,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "lc", "70b", "qwen2-7b", "phi2", "gpt2-xl", "tiny"])
+    ap.add_argument("--config", default="8b", choices=["8b", "8b-k", "8b-km", "lc", "70b", "qwen2-7b", "phi2", "gpt2-xl", "tiny"])
     ap.add_argument("--mode", default="full", choices=["full", "decode", "copy", "micro"])
     ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -316,6 +319,11 @@ def main():
         sp = fwgpu.spec_8b(n_ctx=max(768, n_ctx), linear_type=fwgpu.GGML_Q4_K, embd_type=fwgpu.GGML_Q4_K,
                            output_type=fwgpu.GGML_Q6_K)
         workload = "Llama-3-8B-shape Q4_K greedy decode (Q4_K embedding, Q6_K output)"
+    elif args.config == "8b-km":
+        sp = fwgpu.spec_8b(n_ctx=max(768, n_ctx), linear_type=fwgpu.GGML_Q4_K, embd_type=fwgpu.GGML_Q4_K,
+                           output_type=fwgpu.GGML_Q6_K, mix_type=fwgpu.GGML_Q6_K)
+        workload = ("Llama-3-8B-shape Q4_K_M-layout greedy decode (Q4_K linears, attn_v and ffn_down Q6_K "
+                    "in even layers, Q4_K embedding, Q6_K output)")
     elif args.config == "70b":
         sp = fwgpu.spec_70b(n_ctx=max(384, n_ctx))
         workload = "Llama-3-70B-shape Q4_0 greedy decode (Q8_0 embedding/output)"
@@ -381,6 +389,7 @@ def main():
     gm.status()                     # raises if a launch gave up at a bounded wait: no number from it
     tok_s = args.steps / (total_ms / 1e3)
     bb = {"8b-k": dict(linear_bb=18, embd_bb=18, out_bb=26.25),                      # per 32 values
+          "8b-km": dict(linear_bb=18, embd_bb=18, out_bb=26.25, mix_bb=26.25),
           "gpt2-xl": dict(linear_bb=34)}.get(args.config, {})
     byte_list = [step_bytes(cfg, p, **bb) for p in range(p0, p0 + args.steps)]
     avg_bytes = float(np.mean(byte_list))

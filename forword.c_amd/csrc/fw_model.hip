@@ -146,7 +146,7 @@ struct forword_gpu {
     bool traced = false;
     // persistent step kernel
     bool mk = false;
-    uint32_t mk_wg = 0, mk_tl = 0, mk_th = 0, mk_epoch = 0;
+    uint32_t mk_wg = 0, mk_tl = 0, mk_th = 0, mk_tm = 0, mk_epoch = 0;
     size_t mk_lds = 0;
     MkArgs mka{};
     uint32_t *d_bar = nullptr, *d_mk_err = nullptr, *d_mk_tickets = nullptr, *d_ami = nullptr;
@@ -437,7 +437,7 @@ static int run_steps(forword_gpu_t *h, size_t n)
             MkArgs a = h->mka;
             a.epoch0 = h->mk_epoch;
             a.n_steps = k;
-            HIPCHK(mk_launch(a, h->mk_tl, h->mk_th, h->mk_wg, h->mk_lds, h->stream), "persistent step launch");
+            HIPCHK(mk_launch(a, h->mk_tl, h->mk_th, h->mk_tm, h->mk_wg, h->mk_lds, h->stream), "persistent step launch");
             h->prof_steps = k;
             h->mk_epoch += k * mk_barriers_per_step(h->cfg.n_layer);
             n -= k;
@@ -480,10 +480,19 @@ static int setup_mk(forword_gpu_t *h)
     if ((env && !strcmp(env, "0")) || h->generic) return 0;
     const forword_gpu_config_t &c = h->cfg;
     const uint32_t n = c.n_embd, hd = c.head_dim, L = c.n_layer;
+    // one linear type; attn_v / ffn_down may be Q6_K in some layers (the Q4_K_M
+    // layout), run from re-laid-out copies as the kernel's second layer type
     const uint32_t tl = h->L[0].q.type;
-    for (const Layer &Ly : h->L)
-        for (const Lin *l : { &Ly.q, &Ly.k, &Ly.v, &Ly.o, &Ly.gate, &Ly.up, &Ly.down })
+    uint32_t tm = 0;
+    for (const Layer &Ly : h->L) {
+        for (const Lin *l : { &Ly.q, &Ly.k, &Ly.o, &Ly.gate, &Ly.up })
             if (l->type != tl) return 0;
+        for (const Lin *l : { &Ly.v, &Ly.down }) {
+            if (l->type == tl) continue;
+            if (l->type != kQ6_K) return 0;
+            tm = kQ6_KR;
+        }
+    }
     // attention units: a KV head's query heads in power-of-two sub-groups (any group)
     const uint32_t group = c.n_head / c.n_head_kv;
     uint32_t gs = 8;
@@ -492,7 +501,7 @@ static int setup_mk(forword_gpu_t *h)
     // a Q6_K lm-head runs from a re-laid-out copy (whole super-blocks per row required)
     const bool head_q6k = h->out.type == kQ6_K;
     const uint32_t th = head_q6k ? kQ6_KR : h->out.type;
-    if (!mk_supported(n, c.n_ff, hd, group, tl, th, h->embd.type) || units + 1 > 64) return 0;
+    if (!mk_supported(n, c.n_ff, hd, group, tl, th, h->embd.type, tm) || units + 1 > 64) return 0;
     int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 ||
@@ -503,10 +512,12 @@ static int setup_mk(forword_gpu_t *h)
 
     MkArgs &a = h->mka;
     a.n_layer = L;
-    a.rb_embd = h->L[0].q.row_bytes;
-    a.rb_ff = h->L[0].down.row_bytes;
+    // row strides of the linear type (layer 0's ffn_down may be of the second type)
+    a.rb_embd = type_row_bytes(tl, n);
+    a.rb_ff = type_row_bytes(tl, c.n_ff);
     a.head_w = h->out.w; a.head_rb = h->out.row_bytes; a.out_norm = h->out_norm;
     a.qa_lin = mk_q_align(tl); a.qa_head = mk_q_align(th);
+    a.rb_mix_embd = (uint64_t)(n / 256) * 224; a.rb_mix_ff = (uint64_t)(c.n_ff / 256) * 224;
     a.embd = h->embd.w; a.embd_type = h->embd.type; a.embd_row_bytes = h->embd.row_bytes; a.embd_scale = c.embd_scale;
     a.n_embd = n; a.n_ff = c.n_ff; a.n_head = c.n_head; a.n_kv = c.n_head_kv; a.head_dim = hd;
     a.n_vocab = c.n_vocab; a.n_ctx = (uint32_t)h->n_ctx; a.eps = c.norm_eps;
@@ -524,8 +535,8 @@ static int setup_mk(forword_gpu_t *h)
     if (ns > 256) ns = 256;
     if (ns < 1) ns = 1;
     a.n_splits = ns;
-    const size_t lds = mk_lds_bytes(a, (uint32_t)cus, tl, th);
-    const int wg = lds ? mk_max_workgroups(tl, th, lds) : 0;
+    const size_t lds = mk_lds_bytes(a, (uint32_t)cus, tl, th, tm);
+    const int wg = lds ? mk_max_workgroups(tl, th, tm, lds) : 0;
     if (wg != cus) {
         fprintf(stderr, "forword_gpu: persistent step kernel cannot launch (LDS %zu B); using per-phase kernels\n", lds);
         return 0;
@@ -534,7 +545,22 @@ static int setup_mk(forword_gpu_t *h)
     std::vector<MkLayer> layers(L);
     for (uint32_t l = 0; l < L; l++) {
         const Layer &Ly = h->L[l];
-        layers[l] = MkLayer{ Ly.q.w, Ly.k.w, Ly.v.w, Ly.o.w, Ly.gate.w, Ly.up.w, Ly.down.w, Ly.attn_norm, Ly.ffn_norm };
+        layers[l] = MkLayer{ Ly.q.w, Ly.k.w, Ly.v.w, Ly.o.w, Ly.gate.w, Ly.up.w, Ly.down.w, Ly.attn_norm, Ly.ffn_norm,
+                             0u, 0u };
+        // the second-type tensors of this layer, re-laid out
+        for (int which = 0; which < 2 && tm; which++) {
+            const Lin &li = which ? Ly.down : Ly.v;
+            if (li.type == tl) continue;
+            const uint32_t n_sb = li.in / 256;
+            uint8_t *rp = nullptr;
+            if (dalloc(h, (void **)&rp, (size_t)li.out * n_sb * 224, "Q6_K layer records")) return -1;
+            if (launch_repack_q6k(li.w, li.row_bytes, li.out, n_sb, rp, h->stream) != hipSuccess) {
+                set_err("persistent step kernel: Q6_K repack launch failed");
+                return -1;
+            }
+            (which ? layers[l].wd : layers[l].wv) = rp;
+            layers[l].mix |= which ? MK_MIX_DOWN : MK_MIX_V;
+        }
     }
     if (dalloc(h, (void **)&h->d_layers, layers.size() * sizeof(MkLayer), "layer table") ||
         dalloc(h, (void **)&h->d_bar, (size_t)wg * 128, "barrier flags") ||
@@ -579,6 +605,7 @@ static int setup_mk(forword_gpu_t *h)
     }
     h->mk_tl = tl;
     h->mk_th = th;
+    h->mk_tm = tm;
     h->mk_wg = (uint32_t)wg;
     h->mk_lds = lds;
     h->mk_epoch = 0;

@@ -18,6 +18,8 @@ struct MkGemv {
     uint32_t n_cols;
     uint64_t row_bytes;
     uint32_t qa;             // slice alignment of the phase's weight type (pairs per slice a multiple of it)
+    uint32_t rlo, rhi;       // rows this GEMV computes (a QKV phase with a V of another type runs as two);
+                             // workgroups still split all n_rows, so the partials of both share one layout
 };
 
 enum MkKind : uint32_t { MK_QKV = 0, MK_ATTN = 1, MK_WO = 2, MK_FFN = 3, MK_DOWN = 4, MK_HEAD = 5 };
@@ -27,7 +29,11 @@ enum MkKind : uint32_t { MK_QKV = 0, MK_ATTN = 1, MK_WO = 2, MK_FFN = 3, MK_DOWN
 struct MkLayer {
     const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
     const float *attn_norm, *ffn_norm;
+    uint32_t mix;            // MK_MIX_V / MK_MIX_DOWN: attn_v / ffn_down is of the kernel's second layer type
+    uint32_t pad;
 };
+// Layers of Q4_K_M files: attn_v and ffn_down of some layers are Q6_K.
+enum : uint32_t { MK_MIX_V = 1, MK_MIX_DOWN = 2 };
 
 // A step is 5 phases per layer (QKV ATTN WO FFN DOWN) and the lm-head (HEAD).
 struct MkArgs {
@@ -68,6 +74,8 @@ struct MkArgs {
     uint64_t *prof;          // optional: wall-clock stamp at kernel start, then after every phase
     uint32_t epoch0, n_steps;
     uint32_t qa_lin, qa_head;  // slice alignment of the layer linears' and the lm-head's weight types
+    uint64_t rb_mix_embd;    // row bytes of an attn_v of the second layer type (n_embd columns)
+    uint64_t rb_mix_ff;      // row bytes of an ffn_down of the second layer type (n_ff columns)
 };
 
 // Threads of one workgroup, and how many of them poll barrier flags and load
@@ -78,22 +86,23 @@ constexpr uint32_t kMkPollers = 256;
 // Barriers one token step performs (the host advances its epoch by this much).
 inline uint32_t mk_barriers_per_step(uint32_t n_layer) { return 5 * n_layer + 1; }
 // Whether the persistent kernel supports this model (else the per-kernel path
-// runs): every layer linear of one type, Q4_0/Q5_0/Q8_0/Q4_K linears; lm-head
-// of those types or kQ6_KR (a Q6_K head after launch_repack_q6k).
+// runs): layer linears of one type (Q4_0/Q5_0/Q8_0/Q4_K), except attn_v and
+// ffn_down of some layers of mix_type (0 for none, kQ6_KR for Q6_K copies
+// after launch_repack_q6k); lm-head of those types or kQ6_KR.
 bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
-                  uint32_t head_type, uint32_t embd_type);
+                  uint32_t head_type, uint32_t embd_type, uint32_t mix_type);
 // Dynamic LDS of one workgroup (args fully set up, n_splits included), 0 if
 // the staged input, the partials and weight rings of every phase do not fit.
-size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type);
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type, uint32_t mix_type);
 // Workgroups of one cooperative launch (one per CU), 0 if it cannot launch.
-int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes);
+int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, uint32_t mix_type, size_t lds_bytes);
 // Q6_K matrix [n_rows][n_sb super-blocks] (rows src_rb bytes apart) into
 // kQ6_KR records at dst (n_rows * n_sb * 224 bytes, 4-byte aligned).
 hipError_t launch_repack_q6k(const uint8_t *src, uint64_t src_rb, uint32_t n_rows, uint32_t n_sb, uint8_t *dst,
                              hipStream_t s);
 // Slice alignment of a weight type in the persistent kernel (MkArgs::qa_lin, qa_head).
 uint32_t mk_q_align(uint32_t type);
-hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,
-                     hipStream_t s);
+hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t mix_type, uint32_t n_wg,
+                     size_t lds_bytes, hipStream_t s);
 
 } // namespace fw

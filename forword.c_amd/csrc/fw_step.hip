@@ -246,7 +246,8 @@ __host__ __device__ inline uint32_t n_slices(uint32_t n_cols, uint32_t qa)
 }
 
 struct Map {
-    uint32_t lo, hi;          // rows of this workgroup
+    uint32_t base;            // first row of this workgroup's share (partials are indexed from it)
+    uint32_t lo, hi;          // rows of the share this call computes (a sub-range of it)
     uint32_t Q, P, S;         // pairs per slice, lanes per row (power of two >= Q), slices
     uint32_t slice, sstep;    // this wave's first slice and the stride to its next one
     uint32_t wis, nws;        // this wave's index among its slice's waves, their count
@@ -256,12 +257,14 @@ struct Map {
 
 // Fewer slices than waves: several waves share a slice and split its row
 // groups.  More slices than waves: each wave walks slices wave, wave + 4, ...
-__device__ __forceinline__ Map plan(uint32_t n_rows, uint32_t n_cols, uint32_t qa)
+__device__ __forceinline__ Map plan(const MkGemv &g)
 {
     Map m;
+    const uint32_t n_rows = g.n_rows, n_cols = g.n_cols, qa = g.qa;
     const uint32_t per = mk_rows_per_wg(n_rows, gridDim.x);
-    m.lo = min(n_rows, blockIdx.x * per);
-    m.hi = min(n_rows, m.lo + per);
+    m.base = min(n_rows, blockIdx.x * per);
+    m.lo = max(m.base, g.rlo);
+    m.hi = max(m.lo, min(min(n_rows, m.base + per), g.rhi));
     m.n_pairs = n_cols / 64;
     m.Q = slice_pairs(m.n_pairs, qa);
     m.P = lanes_per_row(m.Q);
@@ -561,7 +564,7 @@ __device__ __forceinline__ void load_x(const float *xs, const Map &m, uint32_t s
 template <uint32_t T, int M>
 __device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint32_t fixed, uint32_t attn_bytes)
 {
-    const Map m = plan(g.n_rows, g.n_cols, g.qa);
+    const Map m = plan(g);
     const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
     const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
     const uint32_t n = min(min(rg.ns, MK_PF), n_sl * m.n_my);
@@ -630,7 +633,7 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
                                      uint32_t attn_bytes, uint32_t n_pre)
 {
     constexpr int D = (int)dma_count(T) * M, NDW = Blk<T>::pair_dw;
-    const Map m = plan(g.n_rows, g.n_cols, g.qa);
+    const Map m = plan(g);
     const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
     const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
     const uint32_t n_items = n_sl * m.n_my;
@@ -668,7 +671,7 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
             lane_sum<M>(acc, m.P);
 #pragma unroll
             for (int mat = 0; mat < M; mat++)
-                if (m.ps == 0 && r < m.hi) part[((r - m.lo) * M + mat) * m.S + sl] = acc[mat];
+                if (m.ps == 0 && r < m.hi) part[((r - m.base) * M + mat) * m.S + sl] = acc[mat];
         }
     }
     __syncthreads();
@@ -1152,6 +1155,8 @@ template <typename T> __device__ __forceinline__ T *uni(T *p)
     return (T *)(((uint64_t)hi << 32) | lo);
 }
 
+__device__ __forceinline__ uint32_t layer_mix(const MkLayer &L) { return __builtin_amdgcn_readfirstlane(L.mix); }
+
 // The matrices of phase `kind` of `layer`.
 __device__ __forceinline__ MkGemv phase_gemv(const MkArgs &a, const MkLayer *tab, uint32_t kind, uint32_t layer)
 {
@@ -1164,10 +1169,11 @@ __device__ __forceinline__ MkGemv phase_gemv(const MkArgs &a, const MkLayer *tab
         g.w[0] = a.head_w;
         g.rows[0] = g.n_rows = a.n_vocab;
         g.row_bytes = a.head_rb;
+        g.rhi = g.n_rows;
         return g;
     }
     const MkLayer &L = tab[layer];
-    const uint32_t kvd = a.n_kv * a.head_dim;
+    const uint32_t kvd = a.n_kv * a.head_dim, mix = layer_mix(L);
     if (kind == MK_QKV) {
         g.w[0] = uni(L.wq); g.w[1] = uni(L.wk); g.w[2] = uni(L.wv);
         g.rows[0] = a.n_embd; g.rows[1] = g.rows[2] = kvd;
@@ -1182,8 +1188,26 @@ __device__ __forceinline__ MkGemv phase_gemv(const MkArgs &a, const MkLayer *tab
         g.w[0] = uni(L.wd);
         g.rows[0] = g.n_rows = a.n_embd;
         g.n_cols = a.n_ff;
-        g.row_bytes = a.rb_ff;
+        g.row_bytes = (mix & MK_MIX_DOWN) ? a.rb_mix_ff : a.rb_ff;
     }
+    // a V of the second type: this descriptor covers the q and k rows, v_part the rest
+    g.rhi = kind == MK_QKV && (mix & MK_MIX_V) ? a.n_embd + kvd : g.n_rows;
+    return g;
+}
+
+// The v rows of a QKV phase whose attn_v is of the second layer type: same
+// workgroup shares as the whole phase (n_rows unchanged), rows past q and k.
+__device__ __forceinline__ MkGemv v_part(const MkArgs &a, const MkGemv &qkv, const MkLayer *tab, uint32_t layer)
+{
+    MkGemv g = qkv;
+    const uint32_t kvd = a.n_kv * a.head_dim;
+    g.w[1] = g.w[2] = uni(tab[layer].wv);
+    g.rows[0] = a.n_embd + kvd;                // rows below are never read here
+    g.rows[1] = kvd;
+    g.rows[2] = 0;
+    g.row_bytes = a.rb_mix_embd;
+    g.rlo = a.n_embd + kvd;
+    g.rhi = g.n_rows;
     return g;
 }
 
@@ -1218,10 +1242,12 @@ __device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, 
 // ending at a grid barrier.  Descriptors are built in registers from the layer
 // table in LDS; the only state carried across a barrier in registers is the
 // next matrix phase's first load batch.
-// TL: type of every linear weight of the layers; TH: type of the lm-head.
-template <uint32_t TL, uint32_t TH>
+// TL: type of the layers' linear weights; TH: type of the lm-head; TM: 0, or
+// the type of the attn_v / ffn_down of layers flagged in MkLayer::mix.
+template <uint32_t TL, uint32_t TH, uint32_t TM>
 __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
 {
+    constexpr uint32_t TMX = TM ? TM : TL;
     extern __shared__ __align__(16) float lds[];
     __shared__ float s_red[MK_WAVES];
     __shared__ uint32_t s_fail;
@@ -1268,6 +1294,8 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                                 : kind == MK_FFN ? uni(tab[layer].ffn_norm)
                                 : kind == MK_HEAD ? a.out_norm : nullptr;
                 const MkGemv g = phase_gemv(a, tab, kind, layer);
+                const uint32_t mix = TM && kind != MK_HEAD ? layer_mix(tab[layer]) : 0u;
+                const bool mixd = kind == MK_DOWN && (mix & MK_MIX_DOWN), mixv = kind == MK_QKV && (mix & MK_MIX_V);
                 if (kind == MK_QKV && layer == 0) {
                     embed(a, xs, x_own, tok, nw, s_red);
                 } else {
@@ -1276,13 +1304,21 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                         if (n_pre) return;
                         if (kind == MK_FFN) n_pre = prefetch<TL, 2>(g, lds8, lay.fixed, lay.attn);
                         else if (kind == MK_HEAD) n_pre = prefetch<TH, 1>(g, lds8, lay.fixed, lay.attn);
+                        else if (mixd) n_pre = prefetch<TMX, 1>(g, lds8, lay.fixed, lay.attn);
                         else n_pre = prefetch<TL, 1>(g, lds8, lay.fixed, lay.attn);
                     };
                     if (!stage(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue)) return;
                 }
-                if (kind == MK_FFN) gemv<TL, 2>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
-                else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
-                else gemv<TL, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                if (kind == MK_FFN) {
+                    gemv<TL, 2>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                } else if (kind == MK_HEAD || mixd) {
+                    if constexpr (TH == TMX) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                    else if (kind == MK_HEAD) gemv<TH, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                    else gemv<TMX, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                } else {
+                    gemv<TL, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
+                }
+                if (mixv) gemv<TMX, 1>(v_part(a, g, tab, layer), xs, part, lds8, lay.fixed, lay.attn, 0);
                 if (kind == MK_QKV)
                     epi_qkv(a, g, part, rope,
                             a.bqkv ? a.bqkv + (size_t)layer * (a.n_embd + 2 * a.n_kv * a.head_dim) : nullptr,
@@ -1365,12 +1401,12 @@ hipError_t launch_repack_q6k(const uint8_t *src, uint64_t src_rb, uint32_t n_row
 
 // ── host side ───────────────────────────────────────────────────────────────
 
-static bool mk_kernel_exists(uint32_t tl, uint32_t th);
+static bool mk_kernel_exists(uint32_t tl, uint32_t th, uint32_t tm);
 
 static bool mk_small_type(uint32_t t) { return t == kQ4_0 || t == kQ5_0 || t == kQ8_0; }
 
 bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t group, uint32_t linear_type,
-                  uint32_t head_type, uint32_t embd_type)
+                  uint32_t head_type, uint32_t embd_type, uint32_t mix_type)
 {
     if (n_embd % 64 || n_ff % 64 || n_embd / 64 > 64 * MK_SMAX || n_ff / 64 > 64 * MK_SMAX) return false;
     if (head_dim != 32 && head_dim != 64 && head_dim != 128) return false;
@@ -1378,10 +1414,11 @@ bool mk_supported(uint32_t n_embd, uint32_t n_ff, uint32_t head_dim, uint32_t gr
     const bool lin_ok = mk_small_type(linear_type) || (linear_type == kQ4_K && n_embd % 256 == 0 && n_ff % 256 == 0);
     const bool head_ok = mk_small_type(head_type) || ((head_type == kQ4_K || head_type == kQ6_KR) && n_embd % 256 == 0);
     const bool embd_ok = mk_small_type(embd_type) || embd_type == kF32 || embd_type == kQ4_K || embd_type == kQ6_K;
-    return lin_ok && head_ok && embd_ok && mk_kernel_exists(linear_type, head_type);
+    const bool mix_ok = mix_type == 0 || (mix_type == kQ6_KR && n_embd % 256 == 0 && n_ff % 256 == 0);
+    return lin_ok && head_ok && embd_ok && mix_ok && mk_kernel_exists(linear_type, head_type, mix_type);
 }
 
-size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type)
+size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32_t head_type, uint32_t mix_type)
 {
     uint32_t part;
     if ((size_t)4 * mk_fixed_floats(a, n_wg, part) + 16 > MK_LDS_BYTES) return 0;
@@ -1391,34 +1428,37 @@ size_t mk_lds_bytes(const MkArgs &a, uint32_t n_wg, uint32_t linear_type, uint32
     const uint32_t re = ring_wave_bytes(L.fixed, ring_base(a.n_embd, L.attn));
     const uint32_t rf = ring_wave_bytes(L.fixed, ring_base(a.n_ff, L.attn));
     if (ring_slots(re, linear_type, 1) < 1 || ring_slots(re, linear_type, 2) < 1 ||
-        ring_slots(rf, linear_type, 1) < 1 || ring_slots(re, head_type, 1) < 1)
+        ring_slots(rf, linear_type, 1) < 1 || ring_slots(re, head_type, 1) < 1 ||
+        (mix_type && (ring_slots(re, mix_type, 1) < 1 || ring_slots(rf, mix_type, 1) < 1)))
         return 0;                                                    // a ring slot for every phase
     return MK_LDS_BYTES;
 }
 
 typedef void (*mk_kernel_t)(MkArgs);
 
-// Instantiated (linear, lm-head) type pairs: the Q4_0/Q5_0/Q8_0 files' pairs,
-// those with a Q6_K head (its repacked form), and Q4_K layers with a Q4_K,
-// Q6_K or Q8_0 head.
-static mk_kernel_t mk_kernel(uint32_t tl, uint32_t th)
+// Instantiated (linear, lm-head, second layer) types: the Q4_0/Q5_0/Q8_0
+// files' pairs, those with a Q6_K head (its repacked form), Q4_K layers with a
+// Q4_K, Q6_K or Q8_0 head, and the Q4_K_M layout (Q4_K layers whose attn_v and
+// ffn_down are Q6_K in some layers, Q6_K head).
+static mk_kernel_t mk_kernel(uint32_t tl, uint32_t th, uint32_t tm)
 {
-#define K(A, B) if (tl == A && th == B) return k_decode<A, B>;
-    K(kQ4_0, kQ4_0) K(kQ4_0, kQ5_0) K(kQ4_0, kQ8_0) K(kQ4_0, kQ6_KR)
-    K(kQ5_0, kQ4_0) K(kQ5_0, kQ5_0) K(kQ5_0, kQ8_0) K(kQ5_0, kQ6_KR)
-    K(kQ8_0, kQ4_0) K(kQ8_0, kQ5_0) K(kQ8_0, kQ8_0) K(kQ8_0, kQ6_KR)
-    K(kQ4_K, kQ4_K) K(kQ4_K, kQ6_KR) K(kQ4_K, kQ8_0)
+#define K(A, B, C) if (tl == A && th == B && tm == C) return k_decode<A, B, C>;
+    K(kQ4_0, kQ4_0, 0) K(kQ4_0, kQ5_0, 0) K(kQ4_0, kQ8_0, 0) K(kQ4_0, kQ6_KR, 0)
+    K(kQ5_0, kQ4_0, 0) K(kQ5_0, kQ5_0, 0) K(kQ5_0, kQ8_0, 0) K(kQ5_0, kQ6_KR, 0)
+    K(kQ8_0, kQ4_0, 0) K(kQ8_0, kQ5_0, 0) K(kQ8_0, kQ8_0, 0) K(kQ8_0, kQ6_KR, 0)
+    K(kQ4_K, kQ4_K, 0) K(kQ4_K, kQ6_KR, 0) K(kQ4_K, kQ8_0, 0)
+    K(kQ4_K, kQ6_KR, kQ6_KR)
 #undef K
     return nullptr;
 }
 
-static bool mk_kernel_exists(uint32_t tl, uint32_t th) { return mk_kernel(tl, th) != nullptr; }
+static bool mk_kernel_exists(uint32_t tl, uint32_t th, uint32_t tm) { return mk_kernel(tl, th, tm) != nullptr; }
 
 uint32_t mk_q_align(uint32_t type) { return q_align(type); }
 
-int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes)
+int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, uint32_t mix_type, size_t lds_bytes)
 {
-    mk_kernel_t k = mk_kernel(linear_type, head_type);
+    mk_kernel_t k = mk_kernel(linear_type, head_type, mix_type);
     int dev = 0, per_cu = 0;
     hipDeviceProp_t p;
     if (!k || lds_bytes > 160 * 1024) return 0;
@@ -1433,10 +1473,10 @@ int mk_max_workgroups(uint32_t linear_type, uint32_t head_type, size_t lds_bytes
     return p.multiProcessorCount;                                  // one workgroup per CU
 }
 
-hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t n_wg, size_t lds_bytes,
-                     hipStream_t s)
+hipError_t mk_launch(const MkArgs &a, uint32_t linear_type, uint32_t head_type, uint32_t mix_type, uint32_t n_wg,
+                     size_t lds_bytes, hipStream_t s)
 {
-    mk_kernel_t k = mk_kernel(linear_type, head_type);
+    mk_kernel_t k = mk_kernel(linear_type, head_type, mix_type);
     if (!k) return hipErrorInvalidValue;
     MkArgs arg = a;
     void *params[] = { &arg };

@@ -24,7 +24,7 @@ ATOL, RTOL = 2e-3, 1e-3
 
 def close(got, exp, what):
     err = np.abs(got.astype(np.float64) - exp.astype(np.float64))
-    bad = err > ATOL + RTOL * np.abs(exp)
+    bad = ~(err <= ATOL + RTOL * np.abs(exp))                  # NaN counts as out of tolerance
     assert not bad.any(), f"{what}: {bad.sum()} elements out of tolerance, max err {err.max():.3g}"
     return float(err.max())
 
