@@ -9,8 +9,9 @@
 // argmax feeds the next token without a host round trip.
 //
 // Two implementations of the step: for models whose layer linears share one
-// Q4_0/Q5_0/Q8_0 type, a persistent cooperative kernel runs whole steps (up to
-// 64 per launch) with grid barriers between phases (fw_step.hip); otherwise
+// Q4_0/Q5_0/Q8_0/Q4_K type (Q4_K with some Q6_K attn_v/ffn_down included), a
+// persistent cooperative kernel runs whole steps (up to 64 per launch) with
+// grid barriers between phases (fw_step.hip); otherwise
 // (or with FORWORD_GPU_MEGAKERNEL=0) one kernel per phase, captured once as a
 // hipGraph and replayed per position.
 #include "fw_kernels.h"

@@ -210,8 +210,10 @@ void *forword_gpu_stream(const forword_gpu_t *h);
 /*
  * Which implementation runs the token step (no counterpart in forword.c, whose
  * step is one C function): 1 = one persistent cooperative kernel per up to 64
- * steps (models whose layer linears share one Q4_0/Q5_0/Q8_0 type, with
- * n_embd and n_ff multiples of 64, head_dim 32/64/128, any GQA group);
+ * steps (models whose layer linears share one Q4_0/Q5_0/Q8_0/Q4_K type, or
+ * Q4_K with some attn_v/ffn_down in Q6_K; a Q4_0/Q5_0/Q8_0/Q4_K/Q6_K lm-head;
+ * n_embd and n_ff multiples of 64, of 256 with K types, head_dim 32/64/128,
+ * any GQA group);
  * 0 = one kernel per phase replayed from a hipGraph.  Setting the environment
  * variable FORWORD_GPU_MEGAKERNEL=0 before forword_gpu_init selects 0.
  */
