@@ -18,6 +18,7 @@ struct MkGemv {
     uint32_t n_cols;
     uint64_t row_bytes;
     uint32_t qa;             // slice alignment of the phase's weight type (pairs per slice a multiple of it)
+    uint32_t qmin;           // pairs per slice at least (up to the row's pairs and 64)
     uint32_t rlo, rhi;       // rows this GEMV computes (a QKV phase with a V of another type runs as two);
                              // workgroups still split all n_rows, so the partials of both share one layout
 };

@@ -20,12 +20,13 @@
 // then LM-HEAD (output RMSNorm folded in) with the argmax reduced by a ticket.
 //
 // GEMV mapping.  A phase's rows are split evenly (even counts, so RoPE pairs
-// stay together) over the workgroups.  Columns are cut into (at most eight
-// per wave set) slices of Q block pairs, Q = pairs / 8 rounded up, so the
-// waves get equal shares; each wave owns a slice, its lanes are (row-in-group,
+// stay together) over the workgroups.  Columns are cut into slices of Q block
+// pairs, Q = pairs / 8 rounded up but at least 32 (the whole row, up to 64
+// pairs, for the lm-head); each wave owns a slice, its lanes are (row-in-group,
 // pair) = (lane / P, lane % P) with P the power of two >= Q (lanes past Q only
 // reload the slice's last pair), so one item of the wave's weight stream
-// covers 64/P rows.  A lane keeps the 64 input values of its pair in
+// covers 64/P rows.  Wide slices give each item long contiguous runs of a row
+// and the lm-head one partial per row.  A lane keeps the 64 input values of its pair in
 // registers for the whole slice, so a wave reads only Q distinct 64-float
 // blocks of the LDS-staged input (stored with a per-block rotation of its
 // 16-byte chunks so those reads are bank-conflict free).  Per-row partial
@@ -51,11 +52,10 @@ constexpr int MK_WAVES = 8;                 // two waves per SIMD, 256 registers
 constexpr int MK_THREADS = MK_WAVES * 64;
 static_assert(MK_THREADS == (int)kMkThreads, "workgroup size");
 static_assert((int)kMkPollers <= MK_THREADS, "one barrier flag per polling thread");
-// Items per wave issued before a barrier for the phase after it.  A CU keeps
-// only some tens of KB of loads in flight: a wave issuing more stalls until
-// earlier ones land, and its own later loads (barrier polls, staged inputs)
-// complete only after its earlier ones.
-constexpr uint32_t MK_PF = 2;
+// Items per wave issued before a barrier (or staging) for the phase after it:
+// the wave's one ring slot.  A wave's own later loads (barrier polls, staged
+// inputs) complete only after its earlier ones.
+constexpr uint32_t MK_PF = 1;
 constexpr int MK_SMAX = 8;                  // column slices per row at most (64 block pairs each)
 
 // threadIdx.x through an opaque move.  Values derived from it are then formed
@@ -220,9 +220,10 @@ __host__ __device__ inline uint32_t mk_rows_per_wg(uint32_t n_rows, uint32_t n_w
 // waves (at most 64 per slice), rounded up to a multiple of qa.  Q4_K slices
 // hold whole super-blocks (qa = 4 quarters): the four lanes of a lane quad then
 // share one super-block, whose header they fetch a dword each.
-__host__ __device__ inline uint32_t slice_pairs(uint32_t n_pairs, uint32_t qa)
+__host__ __device__ inline uint32_t slice_pairs(uint32_t n_pairs, uint32_t qa, uint32_t qmin)
 {
     uint32_t q = (n_pairs + MK_WAVES - 1) / MK_WAVES;
+    if (q < qmin) q = qmin < n_pairs ? qmin : n_pairs;
     q = q < 1 ? 1 : q > 64 ? 64 : q;
     return (q + qa - 1) / qa * qa;
 }
@@ -239,9 +240,9 @@ __host__ __device__ inline uint32_t lanes_per_row(uint32_t q)
 }
 
 // Column slices of a row of n_cols values.
-__host__ __device__ inline uint32_t n_slices(uint32_t n_cols, uint32_t qa)
+__host__ __device__ inline uint32_t n_slices(uint32_t n_cols, uint32_t qa, uint32_t qmin)
 {
-    const uint32_t np = n_cols / 64, q = slice_pairs(np, qa);
+    const uint32_t np = n_cols / 64, q = slice_pairs(np, qa, qmin);
     return (np + q - 1) / q;
 }
 
@@ -266,7 +267,7 @@ __device__ __forceinline__ Map plan(const MkGemv &g)
     m.lo = max(m.base, g.rlo);
     m.hi = max(m.lo, min(min(n_rows, m.base + per), g.rhi));
     m.n_pairs = n_cols / 64;
-    m.Q = slice_pairs(m.n_pairs, qa);
+    m.Q = slice_pairs(m.n_pairs, qa, g.qmin);
     m.P = lanes_per_row(m.Q);
     m.S = (m.n_pairs + m.Q - 1) / m.Q;
     const uint32_t wave = wave_id(), lane = tid() & 63;
@@ -316,7 +317,11 @@ __device__ __forceinline__ const uint8_t *row_ptr(const MkGemv &g, uint32_t r, i
 // HBM straight into the wave's ring of NS slots in LDS (global_load_lds: no
 // registers are held while they are in flight).  When the wave consumes an
 // item it reads the slot into registers and refills it with the item NS
-// places further on, so NS - 1 items stay in flight while it computes.
+// places further on, so NS - 1 items stay in flight while it reads and one
+// while it computes.  NS is 1: every phase, the lm-head included, measured
+// fastest with a single slot per wave (one item landing while one is
+// summed); deeper rings only queued more loads ahead of the latency-bound
+// staging and publishing of the next phase.
 // Vector memory loads complete in order, so the wave waits for an item with
 // s_waitcnt vmcnt((NS - 1) * D), D being the DMA instructions per item.  The
 // compiler does not track LDS written by these DMAs, so these waits are
@@ -340,7 +345,9 @@ __host__ __device__ constexpr uint32_t dma_pair_lds(uint32_t t)
 }
 __host__ __device__ constexpr uint32_t slot_bytes(uint32_t t, uint32_t M) { return M * dma_pair_lds(t); }
 
-constexpr uint32_t MK_NS_MAX = 12;          // ring slots per wave at most
+constexpr uint32_t MK_NS_MAX = 1;           // ring slots per wave at most (see the weight stream notes)
+constexpr uint32_t MK_QMIN_LAYER = 32;      // block pairs per column slice at least: layer phases
+constexpr uint32_t MK_QMIN_HEAD = 64;       // and the lm-head (a whole row of up to 64 pairs)
 constexpr uint32_t MK_VMCNT_MAX = 63;       // largest s_waitcnt vmcnt
 
 // Ring slots of a wave for items of type t with M matrices, given its bytes.
@@ -702,7 +709,7 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols, g.qa), hd = a.head_dim, half = hd / 2;
+    const uint32_t ns = n_slices(g.n_cols, g.qa, g.qmin), hd = a.head_dim, half = hd / 2;
     const uint32_t kvd = a.n_kv * hd, nq = g.rows[0];
     for (uint32_t rl = 2 * tid(); rl < hi - lo; rl += 2 * MK_THREADS) {
         const uint32_t r = lo + rl;
@@ -735,7 +742,7 @@ __device__ __forceinline__ void epi_resid(const MkArgs &a, const MkGemv &g, cons
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols, g.qa);
+    const uint32_t ns = n_slices(g.n_cols, g.qa, g.qmin);
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const uint32_t r = lo + rl;
         const float v = x_own[rl] + row_sum<1>(part, rl, 0, ns);
@@ -760,7 +767,7 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols, g.qa);
+    const uint32_t ns = n_slices(g.n_cols, g.qa, g.qmin);
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const float gv = row_sum<2>(part, rl, 0, ns);
         const float av = a.act == ACT_SILU ? silu_f(gv) : a.act == ACT_GELU ? gelu_erf(gv) : gelu_tanh(gv);
@@ -805,7 +812,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
     __shared__ uint32_t s_last;
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
-    const uint32_t ns = n_slices(g.n_cols, g.qa);
+    const uint32_t ns = n_slices(g.n_cols, g.qa, g.qmin);
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
@@ -1113,12 +1120,12 @@ struct MkLds {
 __host__ __device__ inline uint32_t mk_fixed_floats(const MkArgs &a, uint32_t n_wg, uint32_t &part)
 {
     const uint32_t kvd = a.n_kv * a.head_dim;
-    const uint32_t ql = a.qa_lin;
-    part = mk_rows_per_wg(a.n_vocab, n_wg) * n_slices(a.n_embd, a.qa_head);                   // lm-head
-    const uint32_t c[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg) * n_slices(a.n_embd, ql),   // QKV
-                           mk_rows_per_wg(a.n_ff, n_wg) * 2 * n_slices(a.n_embd, ql),           // gate, up
-                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_embd, ql),             // WO
-                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff, ql) };             // down
+    const uint32_t ql = a.qa_lin, mq = MK_QMIN_LAYER;
+    part = mk_rows_per_wg(a.n_vocab, n_wg) * n_slices(a.n_embd, a.qa_head, MK_QMIN_HEAD);      // lm-head
+    const uint32_t c[] = { mk_rows_per_wg(a.n_embd + 2 * kvd, n_wg) * n_slices(a.n_embd, ql, mq),   // QKV
+                           mk_rows_per_wg(a.n_ff, n_wg) * 2 * n_slices(a.n_embd, ql, mq),           // gate, up
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_embd, ql, mq),             // WO
+                           mk_rows_per_wg(a.n_embd, n_wg) * n_slices(a.n_ff, ql, mq) };             // down
     for (uint32_t v : c) part = v > part ? v : part;
     part = (part + 3) & ~3u;
     return part + a.n_layer * (uint32_t)(sizeof(MkLayer) / 4) + mk_rows_per_wg(a.n_embd, n_wg) + a.head_dim;
@@ -1164,8 +1171,10 @@ __device__ __forceinline__ MkGemv phase_gemv(const MkArgs &a, const MkLayer *tab
     g.n_cols = a.n_embd;
     g.row_bytes = a.rb_embd;
     g.qa = a.qa_lin;
+    g.qmin = MK_QMIN_LAYER;
     if (kind == MK_HEAD) {
         g.qa = a.qa_head;
+        g.qmin = MK_QMIN_HEAD;
         g.w[0] = a.head_w;
         g.rows[0] = g.n_rows = a.n_vocab;
         g.row_bytes = a.head_rb;
