@@ -143,9 +143,10 @@ __device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *
 // are loaded again, in batches with a back-off so early workgroups do not
 // flood memory.  Returns false when a wait gives up or another workgroup has
 // failed (the error word is then set); every thread returns the same.
-constexpr int MK_TB = 16;                   // values per thread per batch
+constexpr int MK_TB_EMBD = 8;               // values per thread per batch: n_embd-wide inputs
+constexpr int MK_TB_FF = 10;                // and the FFN activations (DOWN's input)
 
-template <typename F>
+template <int MK_TB, typename F>
 __device__ __forceinline__ bool stage(const MkArgs &a, float *xs, const uint64_t *src, uint32_t n, const float *nw,
                                       float eps, uint32_t tag, float *s_red, uint32_t *s_fail, F &&issue)
 {
@@ -1316,7 +1317,10 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                         else if (mixd) n_pre = prefetch<TMX, 1>(g, lds8, lay.fixed, lay.attn);
                         else n_pre = prefetch<TL, 1>(g, lds8, lay.fixed, lay.attn);
                     };
-                    if (!stage(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue)) return;
+                    const bool ok = kind == MK_DOWN
+                                        ? stage<MK_TB_FF>(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue)
+                                        : stage<MK_TB_EMBD>(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue);
+                    if (!ok) return;
                 }
                 if (kind == MK_FFN) {
                     gemv<TL, 2>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
