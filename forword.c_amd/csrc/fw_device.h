@@ -67,7 +67,7 @@ __device__ __forceinline__ float2v nib2(uint32_t v)
 // d * sum_j (q_j - 8) x_j over one Q4_0 block; q[4] = the 16 code bytes, x[32].
 __device__ __forceinline__ float dot_q4_0(float d, const uint32_t *q, const float *x, float sx)
 {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    float a0 = 0.f, a1 = 0.f;                    // two chains: fewer adds to close than four
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         uint32_t lo = q[w] & 0x0F0F0F0Fu, hi = (q[w] >> 4) & 0x0F0F0F0Fu;
@@ -75,14 +75,14 @@ __device__ __forceinline__ float dot_q4_0(float d, const uint32_t *q, const floa
         float2v h01 = nib2<false>(hi), h23 = nib2<true>(hi);
         a0 = __builtin_fmaf(l01.x, x[4 * w + 0], a0);
         a1 = __builtin_fmaf(l01.y, x[4 * w + 1], a1);
-        a2 = __builtin_fmaf(l23.x, x[4 * w + 2], a2);
-        a3 = __builtin_fmaf(l23.y, x[4 * w + 3], a3);
+        a0 = __builtin_fmaf(l23.x, x[4 * w + 2], a0);
+        a1 = __builtin_fmaf(l23.y, x[4 * w + 3], a1);
         a0 = __builtin_fmaf(h01.x, x[16 + 4 * w + 0], a0);
         a1 = __builtin_fmaf(h01.y, x[16 + 4 * w + 1], a1);
-        a2 = __builtin_fmaf(h23.x, x[16 + 4 * w + 2], a2);
-        a3 = __builtin_fmaf(h23.y, x[16 + 4 * w + 3], a3);
+        a0 = __builtin_fmaf(h23.x, x[16 + 4 * w + 2], a0);
+        a1 = __builtin_fmaf(h23.y, x[16 + 4 * w + 3], a1);
     }
-    float s = (a0 + a1) + (a2 + a3);              // sum q_j x_j / 512
+    float s = a0 + a1;                           // sum q_j x_j / 512
     return d * __builtin_fmaf(s, 512.0f, -8.0f * sx);
 }
 
