@@ -152,7 +152,9 @@ struct forword_gpu {
     MkArgs mka{};
     uint32_t *d_bar = nullptr, *d_mk_err = nullptr, *d_mk_tickets = nullptr, *d_ami = nullptr;
     float *d_amv = nullptr, *d_mk_part = nullptr;
-    uint64_t *d_tx = nullptr, *d_tatt = nullptr, *d_th = nullptr;   // tagged activations of the persistent kernel
+    uint64_t *d_tx = nullptr, *d_tatt = nullptr;   // tagged activations of the persistent kernel
+    float *d_hf = nullptr;                          // its FFN activations
+    uint32_t *d_hflag = nullptr;                    // and their per-workgroup flags
     MkLayer *d_layers = nullptr;
     uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
     uint32_t prof_steps = 0;
@@ -466,7 +468,7 @@ static int mk_check(forword_gpu_t *h)
     (void)hipMemset(h->d_mk_err, 0, 4);
     (void)hipMemset(h->d_tx, 0, (size_t)h->cfg.n_embd * 8);
     (void)hipMemset(h->d_tatt, 0, (size_t)h->cfg.n_embd * 8);
-    (void)hipMemset(h->d_th, 0, (size_t)h->cfg.n_ff * 8);
+    (void)hipMemset(h->d_hflag, 0, (size_t)h->mk_wg * 128);
     (void)hipDeviceSynchronize();
     h->mk_epoch = 0;
     set_err("persistent step kernel: a grid barrier timed out; results of the last call are invalid");
@@ -570,7 +572,8 @@ static int setup_mk(forword_gpu_t *h)
         dalloc(h, (void **)&h->d_mk_part, (size_t)c.n_head * ns * (hd + 2) * 4, "attention partials") ||
         dalloc(h, (void **)&h->d_tx, (size_t)n * 8, "tagged x") ||
         dalloc(h, (void **)&h->d_tatt, (size_t)n * 8, "tagged attention output") ||
-        dalloc(h, (void **)&h->d_th, (size_t)c.n_ff * 8, "tagged ffn activations"))
+        dalloc(h, (void **)&h->d_hf, (size_t)c.n_ff * 4, "ffn activations") ||
+        dalloc(h, (void **)&h->d_hflag, (size_t)wg * 128, "ffn activation flags"))
         return -1;
     if (head_q6k) {
         const uint32_t n_sb = n / 256;
@@ -583,11 +586,11 @@ static int setup_mk(forword_gpu_t *h)
         a.head_w = rp;
         a.head_rb = (uint64_t)n_sb * 224;
     }
-    a.tx = h->d_tx; a.tatt = h->d_tatt; a.th = h->d_th;
+    a.tx = h->d_tx; a.tatt = h->d_tatt; a.hf = h->d_hf; a.hflag = h->d_hflag;
     if (hipMemcpy(h->d_layers, layers.data(), layers.size() * sizeof(MkLayer), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(h->d_bar, 0, (size_t)wg * 128) != hipSuccess || hipMemset(h->d_mk_tickets, 0, 64 * 4) != hipSuccess ||
         hipMemset(h->d_mk_err, 0, 4) != hipSuccess || hipMemset(h->d_tx, 0, (size_t)n * 8) != hipSuccess ||
-        hipMemset(h->d_tatt, 0, (size_t)n * 8) != hipSuccess || hipMemset(h->d_th, 0, (size_t)c.n_ff * 8) != hipSuccess ||
+        hipMemset(h->d_tatt, 0, (size_t)n * 8) != hipSuccess || hipMemset(h->d_hflag, 0, (size_t)wg * 128) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         set_err("persistent step kernel: device set-up failed");
         return -1;

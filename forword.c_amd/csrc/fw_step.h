@@ -60,8 +60,12 @@ struct MkArgs {
     const float *bqkv;       // [n_layer][n_embd + 2 kv_dim] attn_q|k|v.bias per layer, or null
     float *q, *logits;
     // Activations passed between phases without a grid barrier, as {value,
-    // epoch} words (see tagged()): residual stream x, attention output, ffn h.
-    uint64_t *tx, *tatt, *th;
+    // epoch} words (see tagged()): residual stream x, attention output.
+    uint64_t *tx, *tatt;
+    // The FFN activations h (n_ff floats) with one flag per workgroup (128 bytes
+    // apart) raised to the phase's epoch once its rows are stored.
+    float *hf;
+    uint32_t *hflag;
     float *trace;            // [2 * n_layer][n_embd] residual stream after each residual add
     float *part;             // attention partials [n_head][n_splits][head_dim + 2]
     StepState *state;

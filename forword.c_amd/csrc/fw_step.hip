@@ -41,7 +41,11 @@
 // polled by one thread of every workgroup; the spin is bounded and sets an
 // error flag, after which every workgroup leaves the kernel.  A workgroup
 // raises its flag first and then issues the next phase's first weight items,
-// so the wait overlaps them.
+// so the wait overlaps them.  x and the attention output pass between phases
+// as tagged {value, epoch} words; the FFN activations h (14336 values on the
+// 8B shape, read whole by every workgroup) pass as plain floats behind one
+// such epoch flag per workgroup, read with 16-byte loads: one flag round trip
+// and one load batch instead of three batches of tagged words.
 #include "fw_device.h"
 #include "fw_kernels.h"
 #include "fw_step.h"
@@ -143,8 +147,7 @@ __device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *
 // are loaded again, in batches with a back-off so early workgroups do not
 // flood memory.  Returns false when a wait gives up or another workgroup has
 // failed (the error word is then set); every thread returns the same.
-constexpr int MK_TB_EMBD = 8;               // values per thread per batch: n_embd-wide inputs
-constexpr int MK_TB_FF = 10;                // and the FFN activations (DOWN's input)
+constexpr int MK_TB_EMBD = 8;               // values per thread per batch (n_embd-wide inputs)
 
 template <int MK_TB, typename F>
 __device__ __forceinline__ bool stage(const MkArgs &a, float *xs, const uint64_t *src, uint32_t n, const float *nw,
@@ -205,6 +208,50 @@ __device__ __forceinline__ bool stage(const MkArgs &a, float *xs, const uint64_t
         if (t == 0) atomicOr(a.err, 1u);
         return false;
     }
+    return true;
+}
+
+// xs <- h (DOWN's input, n floats): every thread t below the workgroup count
+// waits for workgroup t's flag to reach `tag` (bounded, like a barrier wait),
+// then the workgroup loads h with 16-byte system-scope loads, up to 8 per
+// thread at once.  Half the bytes of tagged words, and one batch of loads
+// where 14336 tagged words take three.  issue() goes out first, as in stage().
+template <typename F>
+__device__ __forceinline__ bool stage_h(const MkArgs &a, float *xs, uint32_t n, uint32_t tag, uint32_t *s_fail,
+                                        F &&issue)
+{
+    constexpr int NB = 8;
+    const uint32_t t = tid();
+    issue();
+    if (t < gridDim.x) {
+        uint32_t spins = 0;
+        while ((int)(ld_sys(a.hflag + t * 32) - tag) < 0) {
+            if (++spins > (1u << 22) || ((spins & 15) == 0 && ld_sys(a.err) != 0)) {
+                atomicOr(a.err, 1u);
+                *s_fail = 1;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    if (*s_fail) return false;
+    for (uint32_t j0 = 0; j0 < n; j0 += 4 * NB * MK_THREADS) {
+        float4v v[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const uint32_t j = j0 + 4 * (t + b * MK_THREADS);
+            if (j < n)
+                asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v[b]) : "v"(gptr(a.hf) + j) : "memory");
+        }
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const uint32_t j = j0 + 4 * (t + b * MK_THREADS);
+            if (j < n) *reinterpret_cast<float4v *>(xs + swz(j)) = v[b];     // 4 consecutive values stay adjacent
+        }
+    }
+    __syncthreads();
     return true;
 }
 
@@ -772,8 +819,11 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const float gv = row_sum<2>(part, rl, 0, ns);
         const float av = a.act == ACT_SILU ? silu_f(gv) : a.act == ACT_GELU ? gelu_erf(gv) : gelu_tanh(gv);
-        st_sys64(a.th + lo + rl, tagged(av * row_sum<2>(part, rl, 1, ns), tag));
+        st_sys(a.hf + lo + rl, av * row_sum<2>(part, rl, 1, ns));
     }
+    wait_mem();                                   // this wave's rows are stored
+    __syncthreads();
+    if (tid() == 0) st_sys(a.hflag + blockIdx.x * 32, tag);
 }
 
 __device__ __forceinline__ bool am_better_mk(float v1, uint32_t i1, float v2, uint32_t i2)
@@ -1298,7 +1348,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 }
             } else {
                 // one call site per GEMV variant keeps the executed code small
-                const uint64_t *src = kind == MK_WO ? a.tatt : kind == MK_DOWN ? a.th : a.tx;
+                const uint64_t *src = kind == MK_WO ? a.tatt : a.tx;
                 const uint32_t n_in = kind == MK_DOWN ? a.n_ff : a.n_embd;
                 const float *nw = kind == MK_QKV ? uni(tab[layer].attn_norm)
                                 : kind == MK_FFN ? uni(tab[layer].ffn_norm)
@@ -1318,7 +1368,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                         else n_pre = prefetch<TL, 1>(g, lds8, lay.fixed, lay.attn);
                     };
                     const bool ok = kind == MK_DOWN
-                                        ? stage<MK_TB_FF>(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue)
+                                        ? stage_h(a, xs, n_in, epoch, &s_fail, issue)
                                         : stage<MK_TB_EMBD>(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue);
                     if (!ok) return;
                 }
