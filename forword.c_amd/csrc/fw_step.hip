@@ -39,7 +39,9 @@
 // any workgroup of the launch reads it, and caches start clean at launch.
 // Grid barriers are per-workgroup epoch flags on separate cache lines, each
 // polled by one thread of every workgroup; the spin is bounded and sets an
-// error flag, after which every workgroup leaves the kernel.  A workgroup
+// error flag, after which every workgroup leaves the kernel.  After the QKV
+// phase a workgroup with attention items polls only the flags of the
+// workgroups whose rows those items read (attn_wait).  A workgroup
 // raises its flag first and then issues the next phase's first weight items,
 // so the wait overlaps them.  x and the attention output pass between phases
 // as tagged {value, epoch} words; the FFN activations h (14336 values on the
@@ -1154,6 +1156,40 @@ __device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint3
 }
 
 // ── the kernel ───────────────────────────────────────────────────────────────
+// After the QKV phase: instead of a grid barrier, a workgroup with attention
+// items waits only for the workgroups that computed the rows its items read
+// (the q rows of the unit's query heads, the k and v rows of its KV head,
+// whose KV-cache rows at pos they appended); threads 0-63, 64-127 and 128-191
+// poll one flag each of those three row ranges.  Workgroups without an
+// attention item do not wait: WO waits for tagged attention outputs.
+__device__ __forceinline__ bool attn_wait(const MkArgs &a, uint32_t epoch, uint32_t *s_fail, uint32_t pos)
+{
+    const uint32_t items = a.attn_units * attn_splits_at(a, pos);
+    const uint32_t hd = a.head_dim, kvd = a.n_kv * hd, per = mk_rows_per_wg(a.n_embd + 2 * kvd, gridDim.x);
+    const uint32_t n_sub = a.attn_units / a.n_kv, t = tid(), range = t / 64, k = t % 64;
+    for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
+        const uint32_t unit = it % a.attn_units, kvh = unit / n_sub;
+        const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * a.attn_gs;
+        uint32_t r0 = 0, r1 = 0;
+        if (range == 0) { r0 = h0 * hd; r1 = (h0 + a.attn_gs) * hd; }
+        else if (range == 1) { r0 = a.n_embd + kvh * hd; r1 = r0 + hd; }
+        else if (range == 2) { r0 = a.n_embd + kvd + kvh * hd; r1 = r0 + hd; }
+        if (r1 > r0 && r0 / per + k <= (r1 - 1) / per) {
+            const uint32_t w = r0 / per + k;
+            uint32_t spins = 0;
+            while ((int)(ld_sys(a.bar + w * 32) - epoch) < 0) {
+                if (++spins > (1u << 22) || ld_sys(a.err) != 0) {
+                    atomicOr(a.err, 1u);
+                    *s_fail = 1;
+                    break;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    return *s_fail == 0;
+}
+
 
 // LDS of one workgroup (host and device agree on it).  Below byte `fixed`: the
 // staged input of the current phase (floats from 0) or the attention scratch,
@@ -1391,9 +1427,10 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd, tag_out);
                 n_pre = 0;
             }
-            // Grid barriers only before attention (it reads the KV row just
-            // appended) and at the end of a step (the next token); the other
-            // phases wait for their tagged inputs instead.
+            // Flags are raised before attention (it reads the KV row just
+            // appended; attention workgroups wait for the rows' producers
+            // only) and at the end of a step (the next token: a full grid
+            // barrier); the other phases wait for their tagged inputs instead.
             if (kind == MK_QKV || i + 1 == n_ops) {
                 bar_arrive(a, tag_out, &s_fail);
                 // the next matrix phase's first items, in flight across the barrier
@@ -1405,7 +1442,9 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                     const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
                     n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);        // WO, or the first QKV
                 }
-                if (!bar_wait(a, tag_out, &s_fail)) return;
+                if (kind == MK_QKV) {
+                    if (!attn_wait(a, tag_out, &s_fail, pos)) return;
+                } else if (!bar_wait(a, tag_out, &s_fail)) return;
             }
             epoch = tag_out;
             if (stamp) a.prof[1 + step * n_ops + i] = wall_clock64();
