@@ -153,3 +153,26 @@ def test_mixed_type_layers_match_oracle(persistent):
             lg = gm.prefill(prompt)
             assert fw_cpu.argmax(lg) == int(ref_gen[0])
             assert np.array_equal(gm.generate_greedy_batched(prompt, 6), ref_gen)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("mix", [False, True], ids=["q4_k", "q4_k_m"])
+def test_8b_shape_kquant_persistent_vs_oracle(mix):
+    """Llama-3-8B shape with Q4_K linears and embedding and a Q6_K lm-head (and the
+    Q4_K_M layout: attn_v / ffn_down Q6_K in the even layers), on the persistent step
+    kernel: 8 prompt tokens and 8 greedy tokens identical to the oracle run
+    row-parallel on the host, and the last forward's logits within tolerance."""
+    sp = fwgpu.spec_8b(n_ctx=64, linear_type=gs.Q4K, embd_type=gs.Q4K, output_type=gs.Q6K,
+                       mix_type=gs.Q6K if mix else 0)
+    prompt = np.random.default_rng(9).integers(3, 128256, 8).astype(np.uint32)
+    fw_cpu.set_threads(16)
+    with fwgpu.HostModel(synth=sp) as host:
+        with kernel_choice(True), fwgpu.GpuModel(host) as gm:
+            assert gm.persistent
+            got = gm.generate_greedy(prompt, 8)
+            lg = gm.forward(int(got[-1]), len(prompt) + 7)
+        with fw_cpu.OracleModel(host) as om:
+            exp = om.generate_greedy(prompt, 8)
+            ref = om.forward(int(exp[-1]), len(prompt) + 7)
+    assert np.array_equal(got, exp), (got, exp)
+    check_close(lg, ref, "8B K-quant logits")
