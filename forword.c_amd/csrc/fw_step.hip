@@ -5,12 +5,13 @@
 // Why: a decode step is ~4.6 GB of weight reads split over ~200 dependent
 // matrix-vector products.  As separate kernels each pays launch ramp and a
 // full memory round trip with HBM idle in between.  Here each CU keeps its
-// share of every matrix streaming through LDS rings (global_load_lds), and a
+// share of every matrix streaming through LDS (global_load_lds), and a
 // workgroup that arrives at a phase boundary has the first rows of its next
 // phase in flight before it waits.  Two waves per SIMD: while one waits on
 // LDS, a shuffle or its ring, the other computes.
 //
-// Phases per layer, separated by grid barriers:
+// Phases per layer, each waiting only for its own inputs (tagged values or
+// per-workgroup flags, described below):
 //   QKV   input x, RMSNorm folded in; epilogue RoPE + q store + KV append
 //   ATTN  split-K over positions per KV head; the GQA group shares one read of
 //         K/V; the last workgroup to finish a head's splits combines them
