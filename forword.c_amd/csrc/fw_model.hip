@@ -148,11 +148,12 @@ struct forword_gpu {
     // persistent step kernel
     bool mk = false;
     uint32_t mk_wg = 0, mk_tl = 0, mk_th = 0, mk_tm = 0, mk_epoch = 0;
-    size_t mk_lds = 0;
+    size_t mk_lds = 0, mk_tq_bytes = 0, mk_tkv_bytes = 0, mk_tpart_bytes = 0;
     MkArgs mka{};
     uint32_t *d_bar = nullptr, *d_mk_err = nullptr, *d_mk_tickets = nullptr, *d_ami = nullptr;
-    float *d_amv = nullptr, *d_mk_part = nullptr;
+    float *d_amv = nullptr;
     uint64_t *d_tx = nullptr, *d_tatt = nullptr;   // tagged activations of the persistent kernel
+    uint64_t *d_tq = nullptr, *d_tkv = nullptr, *d_tpart = nullptr;   // and of its attention
     float *d_hf = nullptr;                          // its FFN activations
     uint32_t *d_hflag = nullptr;                    // and their per-workgroup flags
     MkLayer *d_layers = nullptr;
@@ -469,6 +470,9 @@ static int mk_check(forword_gpu_t *h)
     (void)hipMemset(h->d_tx, 0, (size_t)h->cfg.n_embd * 8);
     (void)hipMemset(h->d_tatt, 0, (size_t)h->cfg.n_embd * 8);
     (void)hipMemset(h->d_hflag, 0, (size_t)h->mk_wg * 128);
+    (void)hipMemset(h->d_tq, 0, h->mk_tq_bytes);
+    (void)hipMemset(h->d_tkv, 0, h->mk_tkv_bytes);
+    (void)hipMemset(h->d_tpart, 0, h->mk_tpart_bytes);
     (void)hipDeviceSynchronize();
     h->mk_epoch = 0;
     set_err("persistent step kernel: a grid barrier timed out; results of the last call are invalid");
@@ -527,7 +531,7 @@ static int setup_mk(forword_gpu_t *h)
     a.kc = h->d_k; a.vc = h->d_v; a.cos_tab = h->d_cos; a.sin_tab = h->d_sin;
     a.bqkv = h->d_bias;
     a.act = ffn_act_code(c);
-    a.q = h->d_q; a.logits = h->d_logits; a.trace = h->d_trace;
+    a.logits = h->d_logits; a.trace = h->d_trace;
     a.state = h->d_state; a.prompt = h->d_prompt; a.ids = h->d_ids; a.argmax_out = h->d_argmax;
     // (attention unit, split) items: about one per workgroup, >= 8 positions per split
     a.attn_gs = gs;
@@ -565,11 +569,15 @@ static int setup_mk(forword_gpu_t *h)
             layers[l].mix |= which ? MK_MIX_DOWN : MK_MIX_V;
         }
     }
+    h->mk_tq_bytes = (size_t)c.n_head * hd * 8;
+    h->mk_tkv_bytes = (size_t)2 * c.n_head_kv * hd * 8;
+    h->mk_tpart_bytes = (size_t)c.n_head * ns * (hd + 2) * 8;
     if (dalloc(h, (void **)&h->d_layers, layers.size() * sizeof(MkLayer), "layer table") ||
         dalloc(h, (void **)&h->d_bar, (size_t)wg * 128, "barrier flags") ||
         dalloc(h, (void **)&h->d_mk_tickets, 64 * 4, "tickets") || dalloc(h, (void **)&h->d_mk_err, 4, "barrier status") ||
         dalloc(h, (void **)&h->d_amv, (size_t)wg * 4, "argmax") || dalloc(h, (void **)&h->d_ami, (size_t)wg * 4, "argmax") ||
-        dalloc(h, (void **)&h->d_mk_part, (size_t)c.n_head * ns * (hd + 2) * 4, "attention partials") ||
+        dalloc(h, (void **)&h->d_tpart, h->mk_tpart_bytes, "tagged attention partials") ||
+        dalloc(h, (void **)&h->d_tq, h->mk_tq_bytes, "tagged q") || dalloc(h, (void **)&h->d_tkv, h->mk_tkv_bytes, "tagged K/V row") ||
         dalloc(h, (void **)&h->d_tx, (size_t)n * 8, "tagged x") ||
         dalloc(h, (void **)&h->d_tatt, (size_t)n * 8, "tagged attention output") ||
         dalloc(h, (void **)&h->d_hf, (size_t)c.n_ff * 4, "ffn activations") ||
@@ -587,16 +595,18 @@ static int setup_mk(forword_gpu_t *h)
         a.head_rb = (uint64_t)n_sb * 224;
     }
     a.tx = h->d_tx; a.tatt = h->d_tatt; a.hf = h->d_hf; a.hflag = h->d_hflag;
+    a.tq = h->d_tq; a.tkv = h->d_tkv; a.tpart = h->d_tpart;
     if (hipMemcpy(h->d_layers, layers.data(), layers.size() * sizeof(MkLayer), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(h->d_bar, 0, (size_t)wg * 128) != hipSuccess || hipMemset(h->d_mk_tickets, 0, 64 * 4) != hipSuccess ||
         hipMemset(h->d_mk_err, 0, 4) != hipSuccess || hipMemset(h->d_tx, 0, (size_t)n * 8) != hipSuccess ||
         hipMemset(h->d_tatt, 0, (size_t)n * 8) != hipSuccess || hipMemset(h->d_hflag, 0, (size_t)wg * 128) != hipSuccess ||
+        hipMemset(h->d_tq, 0, h->mk_tq_bytes) != hipSuccess || hipMemset(h->d_tkv, 0, h->mk_tkv_bytes) != hipSuccess ||
+        hipMemset(h->d_tpart, 0, h->mk_tpart_bytes) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         set_err("persistent step kernel: device set-up failed");
         return -1;
     }
     a.layers = h->d_layers;
-    a.part = h->d_mk_part;
     a.bar = h->d_bar;
     a.tickets = h->d_mk_tickets;
     a.err = h->d_mk_err;

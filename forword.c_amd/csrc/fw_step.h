@@ -58,21 +58,23 @@ struct MkArgs {
     float *kc, *vc;
     const float *cos_tab, *sin_tab;
     const float *bqkv;       // [n_layer][n_embd + 2 kv_dim] attn_q|k|v.bias per layer, or null
-    float *q, *logits;
+    float *logits;
     // Activations passed between phases without a grid barrier, as {value,
-    // epoch} words (see tagged()): residual stream x, attention output.
-    uint64_t *tx, *tatt;
+    // epoch} words (see tagged()): residual stream x, attention output, q
+    // (n_head * head_dim), the K/V row of the current position ([k | v],
+    // 2 * n_kv * head_dim) and the attention partials
+    // [n_head][n_splits][head_dim + 2] (o, then m and l).
+    uint64_t *tx, *tatt, *tq, *tkv, *tpart;
     // The FFN activations h (n_ff floats) with one flag per workgroup (128 bytes
     // apart) raised to the phase's epoch once its rows are stored.
     float *hf;
     uint32_t *hflag;
     float *trace;            // [2 * n_layer][n_embd] residual stream after each residual add
-    float *part;             // attention partials [n_head][n_splits][head_dim + 2]
     StepState *state;
     const uint32_t *prompt;
     uint32_t *ids, *argmax_out;
     uint32_t *bar;           // one barrier flag per workgroup, 128 bytes apart
-    uint32_t *tickets;       // n_kv attention-combine tickets + 1 argmax ticket, zero between uses
+    uint32_t *tickets;       // argmax ticket at [attn_units], zero between uses
     uint32_t *err;           // set when a barrier or tagged-value wait gives up
     float *am_v;
     uint32_t *am_i;

@@ -12,9 +12,11 @@
 //
 // Phases per layer, each waiting only for its own inputs (tagged values or
 // per-workgroup flags, described below):
-//   QKV   input x, RMSNorm folded in; epilogue RoPE + q store + KV append
+//   QKV   input x, RMSNorm folded in; epilogue RoPE, KV append, q and the new
+//         K/V row published as tagged words
 //   ATTN  split-K over positions per KV head; the GQA group shares one read of
-//         K/V; the last workgroup to finish a head's splits combines them
+//         K/V; partials published as tagged words, which the workgroup of the
+//         head's first split merges
 //   WO    input: attention output; epilogue x += y (+ trace row)
 //   FFN   input x, RMSNorm folded in; gate and up rows together -> silu(g)*u
 //   DOWN  input h; epilogue x += y (+ trace row)
@@ -36,16 +38,18 @@
 // Cross-workgroup data (activations, partials, tickets, flags, step state)
 // moves through system-scope relaxed atomics: the L2s of the eight XCDs are not
 // coherent with each other and an agent-scope release writes back a whole L2.
-// K/V rows are read with plain loads: a row is written (write-through) before
-// any workgroup of the launch reads it, and caches start clean at launch.
+// K/V rows of earlier steps are read with plain loads: a row is written
+// (write-through, ordered by the end-of-step barrier) before any workgroup of
+// the launch reads it, and caches start clean at launch; the row of the
+// current position is read only as tagged words in its own step.
 // Grid barriers are per-workgroup epoch flags on separate cache lines, each
 // polled by one thread of every workgroup; the spin is bounded and sets an
-// error flag, after which every workgroup leaves the kernel.  After the QKV
-// phase a workgroup with attention items polls only the flags of the
-// workgroups whose rows those items read (attn_wait).  A workgroup
-// raises its flag first and then issues the next phase's first weight items,
-// so the wait overlaps them.  x and the attention output pass between phases
-// as tagged {value, epoch} words; the FFN activations h (14336 values on the
+// error flag, after which every workgroup leaves the kernel.  The only grid
+// barrier is at the end of a step; a workgroup raises its flag first and then
+// issues the next step's first weight items, so the wait overlaps them.  x,
+// q, the new K/V row, the attention partials and the attention output pass
+// between phases as tagged {value, epoch} words (an attention item loads its
+// older K/V rows before it polls q); the FFN activations h (14336 values on the
 // 8B shape, read whole by every workgroup) pass as plain floats behind one
 // such epoch flag per workgroup, read with 16-byte loads: one flag round trip
 // and one load batch instead of three batches of tagged words.
@@ -675,8 +679,10 @@ __device__ __forceinline__ void lane_sum(float (&v)[M], uint32_t P)
     }
     if (P >= 32) {
 #pragma unroll
-        for (int i = 0; i < M; i++)                                          // lane ^ 16 (swizzle bit masks)
-            v[i] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[i]), 0x401F));
+        for (int i = 0; i < M; i++) {                                        // lane ^ 16: rows 0+1, 2+3
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+            v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);             // (gfx950 permlane swap, no LDS)
+        }
     }
     if (P >= 64) {
 #pragma unroll
@@ -754,9 +760,10 @@ __device__ __forceinline__ void wg_rows(uint32_t n_rows, uint32_t &lo, uint32_t 
 
 // Bias (linear.c:214-221; bias null when the model has none), RoPE on q/k rows
 // (rope.c:37-43) with this position's cos/sin (rope[0..hd/2) and rope[hd/2..hd)
-// in LDS), q store, K/V append at pos (attention.c:129-140).
+// in LDS), K/V append at pos (attention.c:129-140).  q and the new K/V row are
+// also published as words tagged `tag` for this step's attention.
 __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const float *part, const float *rope,
-                                        const float *bias, uint32_t layer, uint32_t pos)
+                                        const float *bias, uint32_t layer, uint32_t pos, uint32_t tag)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
@@ -776,12 +783,18 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
             v0 = w0;
             v1 = w1;
         }
-        float *dst;
-        if (r < nq) dst = a.q + r;
-        else if (r < nq + kvd) dst = a.kc + ((size_t)layer * a.n_ctx + pos) * kvd + (r - nq);
-        else dst = a.vc + ((size_t)layer * a.n_ctx + pos) * kvd + (r - nq - kvd);
-        st_sys(dst, v0);
-        st_sys(dst + 1, v1);
+        uint64_t *tdst;
+        if (r < nq) {
+            tdst = a.tq + r;
+        } else {
+            float *dst = r < nq + kvd ? a.kc + ((size_t)layer * a.n_ctx + pos) * kvd + (r - nq)
+                                      : a.vc + ((size_t)layer * a.n_ctx + pos) * kvd + (r - nq - kvd);
+            st_sys(dst, v0);
+            st_sys(dst + 1, v1);
+            tdst = a.tkv + (r - nq);
+        }
+        st_sys64(tdst, tagged(v0, tag));
+        st_sys64(tdst + 1, tagged(v1, tag));
     }
 }
 
@@ -930,23 +943,137 @@ __device__ __forceinline__ uint32_t attn_splits_at(const MkArgs &a, uint32_t pos
     return want > a.n_splits ? a.n_splits : want;
 }
 
-// Positions t = first, first + NG, ... below t1 (NG = 2 * MK_WAVES) into the
-// running (m, l, o) of the G heads: a batch of U positions is loaded at once
-// (positions past t1 reload the batch's first one and get no weight), all
-// U * G scores are formed, then each head is rescaled once per batch.
-template <int EPL, int G, int U>
-__device__ __forceinline__ void attn_batches(const FW_GLOBAL float *kc, const FW_GLOBAL float *vc, size_t kvd,
-                                             const float (&qv)[G][EPL], float sc, uint32_t first, uint32_t t1,
-                                             float (&m)[G], float (&l)[G], float (&o)[G][EPL])
+// Waits until the tagged words w[k] (k with bit k of `valid`; the others are
+// left as fresh) carry `tag`: all are loaded at once, the stale ones again in
+// rounds with a back-off.  Returns false when the wait gives up or another
+// workgroup has failed; the error word is then set.
+template <int N, typename F>
+__device__ __forceinline__ bool load_tagged(const MkArgs &a, uint64_t (&w)[N], uint64_t valid, uint32_t tag, F &&addr)
 {
-    constexpr uint32_t NG = 2 * MK_WAVES;
-    for (uint32_t tb = first; tb < t1; tb += U * NG) {
-        float kk[U][EPL], vv[U][EPL];
+#pragma unroll
+    for (int k = 0; k < N; k++) w[k] = (valid >> k) & 1u ? ld_sys64(addr(k)) : (uint64_t)tag << 32;
+    static_assert(N <= 64, "one mask bit per word");
+    uint64_t stale = 0;
+#pragma unroll
+    for (int k = 0; k < N; k++)
+        if ((uint32_t)(w[k] >> 32) != tag) stale |= 1ull << k;
+    for (uint32_t round = 0; stale; round++) {
+        __builtin_amdgcn_s_sleep(8);                               // ~512 cycles
+        if (round > (1u << 16) || ((round & 15) == 15 && ld_sys(a.err) != 0)) {
+            atomicOr(a.err, 1u);
+            return false;
+        }
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if ((stale >> k) & 1u) w[k] = ld_sys64(addr(k));
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if (((stale >> k) & 1u) && (uint32_t)(w[k] >> 32) == tag) stale &= ~(1ull << k);
+    }
+    return true;
+}
+
+__device__ __forceinline__ float untag(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)w); }
+
+// 2^v by the hardware instruction (v_exp_f32): 2^-inf = 0; results below the
+// normal range (weights under 2^-126 of the running maximum) may flush to 0.
+__device__ __forceinline__ float ex2(float v) { return __builtin_amdgcn_exp2f(v); }
+
+// One (KV head, split) item: online softmax (log2 domain) over the split's
+// positions for the G query heads of the group (attention.c:142-164); partial
+// (o[HD], m, l) per query head to a.tpart as words tagged `tag`.  A position
+// is spread over 32 lanes (EPL = HD/32 dimensions each), so a wave walks two
+// positions at a time, U per batch (positions past t1 reload the batch's
+// first one and get no weight).
+// The K/V rows below pos were written in earlier steps, so the first batch of
+// them is loaded before the query; q and the K/V row of pos come from the QKV
+// phase as words tagged `tin` and are polled.  Row pos is never read from the
+// cache in this step: a plain load racing its write would leave a stale line
+// in this XCD's L2 for later steps.
+template <int EPL, int G, int U>
+__device__ __forceinline__ bool attn_item(const MkArgs &a, uint32_t layer, uint32_t pos, uint32_t unit, uint32_t split,
+                                          float *lds, uint32_t tin, uint32_t tag)
+{
+    constexpr uint32_t NG = 2 * MK_WAVES;                  // position streams of the workgroup
+    constexpr int HD = 32 * EPL;
+    const uint32_t n_sub = a.attn_units / a.n_kv, kvh = unit / n_sub;
+    const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * G;     // first query head of the unit
+    float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
+    float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
+    float (*s_l)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD + MK_WAVES * G);
+    const uint32_t n_pos = pos + 1, ns = attn_splits_at(a, pos), chunk = (n_pos + ns - 1) / ns;
+    const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
+    const bool has_pos = t1 == n_pos;                      // the split ends with the new position
+    const int lane = tid() & 63, wave = wave_id(), l32 = lane & 31;
+    const size_t kvd = (size_t)a.n_kv * HD;
+    const FW_GLOBAL float *kc = gptr(a.kc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
+    const FW_GLOBAL float *vc = gptr(a.vc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
+    const float sc = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;     // attention.c:143, in log2 units
+    // Each 32-lane group walks positions first, first + NG, ...
+    const uint32_t first = t0 + wave * 2 + (lane >> 5);
+    auto at = [&](uint32_t tb, int u) { return tb + u * NG < t1 ? tb + u * NG : tb; };
+    float kk[U][EPL], vv[U][EPL];
+    auto load = [&](uint32_t tb) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const uint32_t t = tb + u * NG < t1 ? tb + u * NG : tb;
-            load_vec<EPL>(kc + (size_t)t * kvd, kk[u]);
-            load_vec<EPL>(vc + (size_t)t * kvd, vv[u]);
+            const uint32_t t = at(tb, u);
+            if (t != pos) {
+                load_vec<EPL>(kc + (size_t)t * kvd, kk[u]);
+                load_vec<EPL>(vc + (size_t)t * kvd, vv[u]);
+            }
+        }
+    };
+    if (first < t1) load(first);
+
+    // q (G * HD words) and, for the split holding pos, its K then V row (HD
+    // each) through LDS: every thread polls up to three words.
+    float qv[G][EPL], kn[EPL], vn[EPL];
+    bool ok;
+    {
+        constexpr uint32_t NQ = G * HD;
+        const uint32_t nw = has_pos ? NQ + 2 * HD : NQ, t = tid();
+        static_assert(NQ + 2 * HD <= 3 * MK_THREADS, "three words per thread");
+        uint64_t w[3];
+        auto word = [&](uint32_t j) {
+            return j < NQ ? a.tq + (size_t)h0 * HD + j : a.tkv + (j - NQ >= HD ? kvd : 0) + kvh * HD + (j - NQ) % HD;
+        };
+        ok = load_tagged<3>(a, w, (t < nw ? 1u : 0u) | (t + MK_THREADS < nw ? 2u : 0u) | (t + 2 * MK_THREADS < nw ? 4u : 0u),
+                            tin, [&](int k) { return word(t + k * MK_THREADS); });
+#pragma unroll
+        for (int k = 0; k < 3; k++)
+            if (t + k * MK_THREADS < nw) lds[t + k * MK_THREADS] = untag(w[k]);
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int e = 0; e < EPL; e++) qv[g][e] = lds[g * HD + l32 * EPL + e];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            kn[e] = has_pos ? lds[NQ + l32 * EPL + e] : 0.f;
+            vn[e] = has_pos ? lds[NQ + HD + l32 * EPL + e] : 0.f;
+        }
+    }
+
+    float m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[g][e] = 0.f;
+    }
+    for (uint32_t tb = first; tb < t1; tb += U * NG) {
+        if (tb != first) load(tb);
+        if (has_pos) {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (at(tb, u) == pos) {
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) {
+                        kk[u][e] = kn[e];
+                        vv[u][e] = vn[e];
+                    }
+                }
         }
         float s[U][G];
 #pragma unroll
@@ -968,13 +1095,13 @@ __device__ __forceinline__ void attn_batches(const FW_GLOBAL float *kc, const FW
                 s[u][g] = tb + u * NG < t1 ? s[u][g] * sc : -INFINITY;
                 mx = fmaxf(mx, s[u][g]);                     // finite: position tb is below t1
             }
-            const float c = exp2f(m[g] - mx);
+            const float c = ex2(m[g] - mx);
             l[g] *= c;
 #pragma unroll
             for (int e = 0; e < EPL; e++) o[g][e] *= c;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const float pe = exp2f(s[u][g] - mx);
+                const float pe = ex2(s[u][g] - mx);
                 l[g] += pe;
 #pragma unroll
                 for (int e = 0; e < EPL; e++) o[g][e] = __builtin_fmaf(pe, vv[u][e], o[g][e]);
@@ -982,49 +1109,10 @@ __device__ __forceinline__ void attn_batches(const FW_GLOBAL float *kc, const FW
             m[g] = mx;
         }
     }
-}
-
-// One (KV head, split) item: online softmax (log2 domain) over the split's
-// positions for the G query heads of the group (attention.c:142-164); partial
-// (o[HD], m, l) per query head to a.part.  A position is spread over 32 lanes
-// (EPL = HD/32 dimensions each), so a wave walks two positions at a time.
-template <int EPL, int G>
-__device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint32_t pos, uint32_t unit, uint32_t split, float *lds)
-{
-    const uint32_t n_sub = a.attn_units / a.n_kv, kvh = unit / n_sub;
-    const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * G;     // first query head of the unit
-    constexpr int HD = 32 * EPL;
-    float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
-    float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
-    float (*s_l)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD + MK_WAVES * G);
-    const uint32_t n_pos = pos + 1, ns = attn_splits_at(a, pos), chunk = (n_pos + ns - 1) / ns;
-    const uint32_t t0 = split * chunk, t1 = min(n_pos, t0 + chunk);
-    const int lane = tid() & 63, wave = wave_id(), grp = lane >> 5, l32 = lane & 31;
-    const size_t kvd = (size_t)a.n_kv * HD;
-    const FW_GLOBAL float *kc = gptr(a.kc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
-    const FW_GLOBAL float *vc = gptr(a.vc) + (size_t)layer * a.n_ctx * kvd + kvh * HD + l32 * EPL;
-    const float sc = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;     // attention.c:143, in log2 units
-
-    float qv[G][EPL], m[G], l[G], o[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        m[g] = -INFINITY;
-        l[g] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) {
-            qv[g][e] = ld_sys(a.q + (h0 + g) * HD + l32 * EPL + e);
-            o[g][e] = 0.f;
-        }
-    }
-    // Each 32-lane group walks positions first, first + 2 * MK_WAVES, ...; in
-    // batches of U (more for long splits).
-    const uint32_t first = t0 + wave * 2 + grp, per_group = (t1 - t0 + 2 * MK_WAVES - 1) / (2 * MK_WAVES);
-    if (per_group <= 2) attn_batches<EPL, G, 2>(kc, vc, kvd, qv, sc, first, t1, m, l, o);
-    else attn_batches<EPL, G, EPL == 4 ? 4 : 8>(kc, vc, kvd, qv, sc, first, t1, m, l, o);
 #pragma unroll
     for (int g = 0; g < G; g++) {                          // merge the wave's two position groups
         const float mw = fmaxf(m[g], __shfl_xor(m[g], 32, 64));
-        const float c = mw == -INFINITY ? 0.f : exp2f(m[g] - mw);
+        const float c = mw == -INFINITY ? 0.f : ex2(m[g] - mw);
         float lw = l[g] * c;
         lw += __shfl_xor(lw, 32, 64);
 #pragma unroll
@@ -1036,7 +1124,7 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
         m[g] = mw;
         l[g] = lw;
     }
-    __syncthreads();                                       // LDS is free (staging / previous item)
+    __syncthreads();                                       // LDS is free (q, previous item)
     if (lane < 32) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -1054,38 +1142,61 @@ __device__ __forceinline__ void attn_item(const MkArgs &a, uint32_t layer, uint3
         float L = 0.f, O = 0.f;
 #pragma unroll
         for (int w = 0; w < MK_WAVES; w++) {
-            const float c = M == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+            const float c = M == -INFINITY ? 0.f : ex2(s_m[w][g] - M);
             L = __builtin_fmaf(s_l[w][g], c, L);
             O = __builtin_fmaf(s_o[w][g][dd], c, O);
         }
-        float *pp = a.part + ((size_t)(h0 + g) * ns + split) * (HD + 2);
-        st_sys(pp + dd, O);
-        if (dd == 0) { st_sys(pp + HD, M); st_sys(pp + HD + 1, L); }
+        uint64_t *pp = a.tpart + ((size_t)(h0 + g) * ns + split) * (HD + 2);
+        st_sys64(pp + dd, tagged(O, tag));
+        if (dd == 0) {
+            st_sys64(pp + HD, tagged(M, tag));
+            st_sys64(pp + HD + 1, tagged(L, tag));
+        }
     }
-    wait_mem();
     __syncthreads();
+    return ok;
 }
 
-// Merge the splits of KV head kvh's G query heads into a.tatt (tagged): every split's
-// (m, l) in one batch of loads, then each thread's o values in batches of 32.
+// Merge the splits of a unit's G query heads into a.tatt (tagged): each thread
+// polls the o values of its (head, dimension) for up to SB splits at once and
+// the first G * ns threads also the (m, l) words, which go to LDS for the split
+// weights; then O = sum over splits of o * w in split order, divided by the
+// weighted sum of the l.
 template <int EPL, int G>
-__device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t unit, float *lds, uint32_t tag, uint32_t pos)
+__device__ __forceinline__ bool attn_combine(const MkArgs &a, uint32_t unit, float *lds, uint32_t tag, uint32_t pos)
 {
-    constexpr int HD = 32 * EPL, SB = 32;
+    constexpr int HD = 32 * EPL, SB = 16;
     const uint32_t ns = attn_splits_at(a, pos);
     const uint32_t n_sub = a.attn_units / a.n_kv;
     const uint32_t h0 = (unit / n_sub) * (a.n_head / a.n_kv) + (unit % n_sub) * G;
     float *s_w = lds;                                      // [G][ns] m, then the split weights
     float *s_l = lds + G * ns;                             // [G][ns] l
     float *s_inv = lds + 2 * G * ns;                       // [G] 1 / sum of weights
-    const float *base = a.part + (size_t)h0 * ns * (HD + 2);      // (head h0+g, split s) at (g*ns + s)*(HD+2)
-    for (uint32_t t = tid(); t < G * ns; t += MK_THREADS) {
-        const float2v ml = ld_sys2(base + (size_t)t * (HD + 2) + HD);
-        s_w[t] = ml[0];
-        s_l[t] = ml[1];
+    const uint64_t *base = a.tpart + (size_t)h0 * ns * (HD + 2);  // (head h0+g, split s) at (g*ns + s)*(HD+2)
+    const uint32_t t = tid(), nb = ns < (uint32_t)SB ? ns : (uint32_t)SB;
+    uint64_t w[SB + 2];
+    bool ok = true;
+    {
+        const uint32_t g = t / HD, d = t % HD;
+        uint64_t valid = 0;
+        if (t < (uint32_t)(G * HD)) valid |= (1ull << nb) - 1u;
+        if (t < G * ns) valid |= 3ull << SB;
+        ok = load_tagged<SB + 2>(a, w, valid, tag, [&](int k) {
+            return k < SB ? base + ((size_t)g * ns + k) * (HD + 2) + d : base + (size_t)t * (HD + 2) + HD + (k - SB);
+        });
+        if (t < G * ns) {
+            s_w[t] = untag(w[SB]);
+            s_l[t] = untag(w[SB + 1]);
+        }
+        for (uint32_t j = t + MK_THREADS; j < G * ns; j += MK_THREADS) {     // more than one (m, l) per thread
+            uint64_t ml[2];
+            ok = load_tagged<2>(a, ml, 3ull, tag, [&](int k) { return base + (size_t)j * (HD + 2) + HD + k; }) && ok;
+            s_w[j] = untag(ml[0]);
+            s_l[j] = untag(ml[1]);
+        }
     }
     __syncthreads();
-    const int lane = tid() & 63;
+    const int lane = t & 63;
     for (uint32_t g = wave_id(); g < (uint32_t)G; g += MK_WAVES) {
         float M = -INFINITY;
         for (uint32_t s = lane; s < ns; s += 64) M = fmaxf(M, s_w[g * ns + s]);
@@ -1093,104 +1204,80 @@ __device__ __forceinline__ void attn_combine(const MkArgs &a, uint32_t unit, flo
         float L = 0.f;
         for (uint32_t s = lane; s < ns; s += 64) {
             const float ms = s_w[g * ns + s];
-            const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-            s_w[g * ns + s] = w;
-            L = __builtin_fmaf(s_l[g * ns + s], w, L);
+            const float wt = ms == -INFINITY ? 0.f : exp2f(ms - M);
+            s_w[g * ns + s] = wt;
+            L = __builtin_fmaf(s_l[g * ns + s], wt, L);
         }
         L = wave_sum(L);
         if (lane == 0) s_inv[g] = 1.0f / L;
     }
     __syncthreads();
-    for (uint32_t i = tid(); i < (uint32_t)(G * HD); i += MK_THREADS) {
+    for (uint32_t i = t; i < (uint32_t)(G * HD); i += MK_THREADS) {
         const uint32_t g = i / HD, d = i % HD;
-        const float *pp = base + (size_t)g * ns * (HD + 2) + d;
-        const float *w = s_w + g * ns;
+        const uint64_t *pp = base + (size_t)g * ns * (HD + 2) + d;
+        const float *wt = s_w + g * ns;
         float O = 0.f;
         for (uint32_t s0 = 0; s0 < ns; s0 += SB) {
-            float v[SB];
-#pragma unroll
-            for (int k = 0; k < SB; k++) v[k] = s0 + k < ns ? ld_sys(pp + (size_t)(s0 + k) * (HD + 2)) : 0.f;
+            if (i != t || s0) {                            // the first batch of the first element is here
+                const uint32_t n = ns - s0 < (uint32_t)SB ? ns - s0 : (uint32_t)SB;
+                ok = load_tagged<SB + 2>(a, w, (1ull << n) - 1u, tag,
+                                         [&](int k) { return pp + (size_t)(s0 + k) * (HD + 2); }) && ok;
+            }
 #pragma unroll
             for (int k = 0; k < SB; k++)
-                if (s0 + k < ns) O = __builtin_fmaf(v[k], w[s0 + k], O);
+                if (s0 + k < ns) O = __builtin_fmaf(untag(w[k]), wt[s0 + k], O);
         }
         st_sys64(a.tatt + (size_t)(h0 + g) * HD + d, tagged(O * s_inv[g], tag));
     }
     __syncthreads();
+    return ok;
 }
 
+// Every (unit, split) item of this workgroup, then the combine of units
+// blockIdx.x, blockIdx.x + gridDim.x, ... (after the items, so a workgroup
+// never waits for an item of its own).  Returns false when a wait gave up.
 template <int EPL, int G>
-__device__ __forceinline__ void attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
+__device__ __forceinline__ bool attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tin,
+                                            uint32_t tag, uint32_t *s_fail)
 {
-    __shared__ uint32_t s_last;
-    const uint32_t items = a.attn_units * attn_splits_at(a, pos);
+    const uint32_t ns = attn_splits_at(a, pos), items = a.attn_units * ns;
+    const uint32_t per_group = ((pos + ns) / ns + 2 * MK_WAVES - 1) / (2 * MK_WAVES);   // positions per lane group
+    bool ok = true;
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
         const uint32_t unit = it % a.attn_units, split = it / a.attn_units;
-        attn_item<EPL, G>(a, layer, pos, unit, split, lds);
-        if (tid() == 0) s_last = ticket_sys(a.tickets + unit) == attn_splits_at(a, pos) - 1;
-        __syncthreads();
-        if (s_last) {
-            attn_combine<EPL, G>(a, unit, lds, tag, pos);
-            if (tid() == 0) st_sys(a.tickets + unit, 0u);
-        }
+        if (per_group <= 2) ok = attn_item<EPL, G, 2>(a, layer, pos, unit, split, lds, tin, tag) && ok;
+        else ok = attn_item<EPL, G, EPL == 4 ? 4 : 8>(a, layer, pos, unit, split, lds, tin, tag) && ok;
     }
-}
-
-template <int EPL>
-__device__ __forceinline__ void attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
-{
-    switch (a.attn_gs) {
-    case 1: attention_t<EPL, 1>(a, layer, pos, lds, tag); break;
-    case 2: attention_t<EPL, 2>(a, layer, pos, lds, tag); break;
-    case 4: attention_t<EPL, 4>(a, layer, pos, lds, tag); break;
-    default: attention_t<EPL, 8>(a, layer, pos, lds, tag); break;
-    }
-}
-
-__device__ __forceinline__ void attention(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tag)
-{
-    switch (a.head_dim) {
-    case 32: attention_e<1>(a, layer, pos, lds, tag); break;
-    case 64: attention_e<2>(a, layer, pos, lds, tag); break;
-    default: attention_e<4>(a, layer, pos, lds, tag); break;
-    }
-}
-
-// ── the kernel ───────────────────────────────────────────────────────────────
-// After the QKV phase: instead of a grid barrier, a workgroup with attention
-// items waits only for the workgroups that computed the rows its items read
-// (the q rows of the unit's query heads, the k and v rows of its KV head,
-// whose KV-cache rows at pos they appended); threads 0-63, 64-127 and 128-191
-// poll one flag each of those three row ranges.  Workgroups without an
-// attention item do not wait: WO waits for tagged attention outputs.
-__device__ __forceinline__ bool attn_wait(const MkArgs &a, uint32_t epoch, uint32_t *s_fail, uint32_t pos)
-{
-    const uint32_t items = a.attn_units * attn_splits_at(a, pos);
-    const uint32_t hd = a.head_dim, kvd = a.n_kv * hd, per = mk_rows_per_wg(a.n_embd + 2 * kvd, gridDim.x);
-    const uint32_t n_sub = a.attn_units / a.n_kv, t = tid(), range = t / 64, k = t % 64;
-    for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
-        const uint32_t unit = it % a.attn_units, kvh = unit / n_sub;
-        const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * a.attn_gs;
-        uint32_t r0 = 0, r1 = 0;
-        if (range == 0) { r0 = h0 * hd; r1 = (h0 + a.attn_gs) * hd; }
-        else if (range == 1) { r0 = a.n_embd + kvh * hd; r1 = r0 + hd; }
-        else if (range == 2) { r0 = a.n_embd + kvd + kvh * hd; r1 = r0 + hd; }
-        if (r1 > r0 && r0 / per + k <= (r1 - 1) / per) {
-            const uint32_t w = r0 / per + k;
-            uint32_t spins = 0;
-            while ((int)(ld_sys(a.bar + w * 32) - epoch) < 0) {
-                if (++spins > (1u << 22) || ld_sys(a.err) != 0) {
-                    atomicOr(a.err, 1u);
-                    *s_fail = 1;
-                    break;
-                }
-            }
-        }
-    }
+    for (uint32_t unit = blockIdx.x; unit < a.attn_units; unit += gridDim.x)
+        ok = attn_combine<EPL, G>(a, unit, lds, tag, pos) && ok;
+    if (!ok) *s_fail = 1;
     __syncthreads();
     return *s_fail == 0;
 }
 
+template <int EPL>
+__device__ __forceinline__ bool attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tin,
+                                            uint32_t tag, uint32_t *s_fail)
+{
+    switch (a.attn_gs) {
+    case 1: return attention_t<EPL, 1>(a, layer, pos, lds, tin, tag, s_fail);
+    case 2: return attention_t<EPL, 2>(a, layer, pos, lds, tin, tag, s_fail);
+    case 4: return attention_t<EPL, 4>(a, layer, pos, lds, tin, tag, s_fail);
+    default: return attention_t<EPL, 8>(a, layer, pos, lds, tin, tag, s_fail);
+    }
+}
+
+__device__ __forceinline__ bool attention(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tin,
+                                          uint32_t tag, uint32_t *s_fail)
+{
+    switch (a.head_dim) {                                  // dimensions per lane: head_dim / 32
+    case 32: return attention_e<1>(a, layer, pos, lds, tin, tag, s_fail);
+    case 64: return attention_e<2>(a, layer, pos, lds, tin, tag, s_fail);
+    default: return attention_e<4>(a, layer, pos, lds, tin, tag, s_fail);
+    }
+}
+
+// ── the kernel ───────────────────────────────────────────────────────────────
 
 // LDS of one workgroup (host and device agree on it).  Below byte `fixed`: the
 // staged input of the current phase (floats from 0) or the attention scratch,
@@ -1377,7 +1464,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
             const uint32_t kind = phase_kind(a, i), layer = i / 5;
             const uint32_t tag_out = epoch + 1;                // tag of the values this phase publishes
             if (kind == MK_ATTN) {
-                attention(a, layer, pos, lds, tag_out);
+                if (!attention(a, layer, pos, lds, epoch, tag_out, &s_fail)) return;
             } else if (kind == MK_HEAD && skip_head) {
                 if (blockIdx.x == 0 && tid() == 0) {
                     st_sys(&a.state->token, a.prompt[pos + 1]);
@@ -1422,30 +1509,24 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 if (kind == MK_QKV)
                     epi_qkv(a, g, part, rope,
                             a.bqkv ? a.bqkv + (size_t)layer * (a.n_embd + 2 * a.n_kv * a.head_dim) : nullptr,
-                            layer, pos);
+                            layer, pos, tag_out);
                 else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out);
                 else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
                 else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd, tag_out);
                 n_pre = 0;
             }
-            // Flags are raised before attention (it reads the KV row just
-            // appended; attention workgroups wait for the rows' producers
-            // only) and at the end of a step (the next token: a full grid
-            // barrier); the other phases wait for their tagged inputs instead.
-            if (kind == MK_QKV || i + 1 == n_ops) {
+            // A full grid barrier only at the end of a step (the next token);
+            // every phase in between waits for its tagged or flagged inputs.
+            // The next matrix phase's first items go out ahead of the wait: the
+            // first QKV across the barrier, and WO across attention (not by a
+            // workgroup with an attention item: its K/V loads would queue
+            // behind these DMAs).
+            if (i + 1 == n_ops) {
                 bar_arrive(a, tag_out, &s_fail);
-                // the next matrix phase's first items, in flight across the barrier
-                // (not by a workgroup with an attention item: its KV loads
-                // would queue behind these DMAs)
-                const bool wrap = i + 1 == n_ops;
-                if (wrap ? step + 1 < a.n_steps : blockIdx.x >= a.attn_units * attn_splits_at(a, pos)) {
-                    const uint32_t ni = wrap ? 0 : i + 2, nk = phase_kind(a, ni);   // past attention
-                    const MkGemv ng = phase_gemv(a, tab, nk, ni / 5);
-                    n_pre = prefetch<TL, 1>(ng, lds8, lay.fixed, lay.attn);        // WO, or the first QKV
-                }
-                if (kind == MK_QKV) {
-                    if (!attn_wait(a, tag_out, &s_fail, pos)) return;
-                } else if (!bar_wait(a, tag_out, &s_fail)) return;
+                if (step + 1 < a.n_steps) n_pre = prefetch<TL, 1>(phase_gemv(a, tab, MK_QKV, 0), lds8, lay.fixed, lay.attn);
+                if (!bar_wait(a, tag_out, &s_fail)) return;
+            } else if (kind == MK_QKV && blockIdx.x >= a.attn_units * attn_splits_at(a, pos)) {
+                n_pre = prefetch<TL, 1>(phase_gemv(a, tab, MK_WO, layer), lds8, lay.fixed, lay.attn);
             }
             epoch = tag_out;
             if (stamp) a.prof[1 + step * n_ops + i] = wall_clock64();
