@@ -304,15 +304,19 @@ __host__ __device__ inline uint32_t n_slices(uint32_t n_cols, uint32_t qa, uint3
 struct Map {
     uint32_t base;            // first row of this workgroup's share (partials are indexed from it)
     uint32_t lo, hi;          // rows of the share this call computes (a sub-range of it)
-    uint32_t Q, P, S;         // pairs per slice, lanes per row (power of two >= Q), slices
-    uint32_t slice, sstep;    // this wave's first slice and the stride to its next one
-    uint32_t wis, nws;        // this wave's index among its slice's waves, their count
+    uint32_t Q, P, S, R;      // pairs per slice, lanes per row (power of two >= Q), slices, rows per group
     uint32_t ps, rs;          // this lane's pair in the slice, row in the group
-    uint32_t n_pairs, n_my;   // pairs per row; row groups this wave walks per slice
+    uint32_t n_pairs;         // pairs per row
+    // This wave's items, (slice, row group) pairs: from (s0, g0) the group
+    // advances by gstep and at gend wraps to gstart on slice s + sstep; n_items in all.
+    uint32_t s0, g0, gstart, gstep, gend, sstep, n_items;
 };
 
-// Fewer slices than waves: several waves share a slice and split its row
-// groups.  More slices than waves: each wave walks slices wave, wave + 4, ...
+// Items of a wave.  Slices that divide the waves: each slice's waves split
+// its row groups (interleaved).  More slices than waves: each wave walks
+// slices wave, wave + 8, ...  Otherwise (3, 5, 6 or 7 slices, e.g. 8B's
+// ffn_down in 7): each wave takes an equal run of the (slice, group) items in
+// slice order, so no wave has more than one item above the mean.
 __device__ __forceinline__ Map plan(const MkGemv &g)
 {
     Map m;
@@ -324,29 +328,32 @@ __device__ __forceinline__ Map plan(const MkGemv &g)
     m.n_pairs = n_cols / 64;
     m.Q = slice_pairs(m.n_pairs, qa, g.qmin);
     m.P = lanes_per_row(m.Q);
+    m.R = 64 / m.P;
     m.S = (m.n_pairs + m.Q - 1) / m.Q;
     const uint32_t wave = wave_id(), lane = tid() & 63;
-    if (m.S <= (uint32_t)MK_WAVES) {
-        m.slice = wave % m.S;
-        m.sstep = MK_SMAX;
-        m.wis = wave / m.S;
-        m.nws = MK_WAVES / m.S + (m.slice < MK_WAVES % m.S ? 1u : 0u);
-    } else {
-        m.slice = wave;
-        m.sstep = MK_WAVES;
-        m.wis = 0;
-        m.nws = 1;
-    }
     m.ps = lane & (m.P - 1);
     m.rs = lane / m.P;
-    const uint32_t R = 64 / m.P, n_groups = (m.hi - m.lo + R - 1) / R;
-    m.n_my = m.wis < n_groups ? (n_groups - m.wis + m.nws - 1) / m.nws : 0;
+    const uint32_t n_groups = (m.hi - m.lo + m.R - 1) / m.R;
+    if (m.S > (uint32_t)MK_WAVES) {
+        m.s0 = wave; m.g0 = 0; m.gstart = 0; m.gstep = 1; m.gend = n_groups; m.sstep = MK_WAVES;
+        m.n_items = (m.S - wave + MK_WAVES - 1) / MK_WAVES * n_groups;
+    } else if (MK_WAVES % m.S == 0) {
+        const uint32_t wis = wave / m.S, nws = MK_WAVES / m.S;
+        const uint32_t n_my = wis < n_groups ? (n_groups - wis + nws - 1) / nws : 0;
+        m.s0 = wave % m.S; m.g0 = wis; m.gstart = wis; m.gstep = nws; m.gend = wis + n_my * nws; m.sstep = MK_SMAX;
+        m.n_items = n_my;
+    } else {
+        const uint32_t n = m.S * n_groups, j0 = wave * n / MK_WAVES, j1 = (wave + 1) * n / MK_WAVES;
+        m.s0 = n_groups ? j0 / n_groups : 0; m.g0 = n_groups ? j0 % n_groups : 0;
+        m.gstart = 0; m.gstep = 1; m.gend = n_groups; m.sstep = 1;
+        m.n_items = j1 - j0;
+    }
     return m;
 }
 
-__device__ __forceinline__ uint32_t map_row(const Map &m, uint32_t k)
+__device__ __forceinline__ uint32_t map_row(const Map &m, uint32_t grp)
 {
-    return m.lo + (m.wis + k * m.nws) * (64 / m.P) + m.rs;
+    return m.lo + grp * m.R + m.rs;
 }
 
 template <int M>
@@ -447,12 +454,14 @@ __device__ __forceinline__ Ring ring_of(uint8_t *lds, uint32_t fixed, uint32_t a
 // Position of an item: slice index among the wave's slices, row group in the
 // slice, ring slot.
 struct Cur {
-    uint32_t si, k, slot;
+    uint32_t s, g, slot;      // slice, row group, ring slot of an item
 };
 
-__device__ __forceinline__ void advance(Cur &c, uint32_t n_my, uint32_t ns)
+__device__ __forceinline__ Cur cur0(const Map &m) { return Cur{m.s0, m.g0, 0}; }
+__device__ __forceinline__ void advance(Cur &c, const Map &m, uint32_t ns)
 {
-    if (++c.k == n_my) { c.k = 0; c.si++; }
+    c.g += m.gstep;
+    if (c.g >= m.gend) { c.g = m.gstart; c.s += m.sstep; }
     if (++c.slot == ns) c.slot = 0;
 }
 
@@ -512,9 +521,8 @@ __device__ __forceinline__ void dma_pair(const uint8_t *row, uint32_t pair, uint
 template <uint32_t T, int M>
 __device__ __forceinline__ void dma_item(const MkGemv &g, const Map &m, const Cur &c, uint8_t *ring)
 {
-    const uint32_t sl = m.slice + c.si * m.sstep;
-    const uint32_t pair = min(sl * m.Q + min(m.ps, m.Q - 1), m.n_pairs - 1);   // lanes past Q reload the last
-    const uint32_t r = min(map_row(m, c.k), m.hi - 1);
+    const uint32_t pair = min(c.s * m.Q + min(m.ps, m.Q - 1), m.n_pairs - 1);   // lanes past Q reload the last
+    const uint32_t r = min(map_row(m, c.g), m.hi - 1);
     uint8_t *slot = ring + c.slot * slot_bytes(T, M);
 #pragma unroll
     for (int mat = 0; mat < M; mat++)
@@ -628,12 +636,11 @@ __device__ __forceinline__ uint32_t prefetch(const MkGemv &g, uint8_t *lds, uint
 {
     const Map m = plan(g);
     const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
-    const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
-    const uint32_t n = min(min(rg.ns, MK_PF), n_sl * m.n_my);
-    Cur c{0, 0, 0};
+    const uint32_t n = min(min(rg.ns, MK_PF), m.n_items);
+    Cur c = cur0(m);
     for (uint32_t i = 0; i < n; i++) {
         dma_item<T, M>(g, m, c, rg.base);
-        advance(c, m.n_my, rg.ns);
+        advance(c, m, rg.ns);
     }
     return n;
 }
@@ -699,44 +706,46 @@ __device__ __forceinline__ void gemv(const MkGemv &g, const float *xs, float *pa
     constexpr int D = (int)dma_count(T) * M, NDW = Blk<T>::pair_dw;
     const Map m = plan(g);
     const Ring rg = ring_of<T, M>(lds, fixed, attn_bytes, g.n_cols);
-    const uint32_t n_sl = m.slice < m.S ? (m.S - m.slice + m.sstep - 1) / m.sstep : 0;
-    const uint32_t n_items = n_sl * m.n_my;
-    Cur is{0, 0, 0};
-    for (uint32_t i = 0; i < n_pre; i++) advance(is, m.n_my, rg.ns);
+    const uint32_t n_items = m.n_items;
+    Cur is = cur0(m);
+    for (uint32_t i = 0; i < n_pre; i++) advance(is, m, rg.ns);
     for (uint32_t i = n_pre; i < min(rg.ns, n_items); i++) {
         dma_item<T, M>(g, m, is, rg.base);
-        advance(is, m.n_my, rg.ns);
+        advance(is, m, rg.ns);
     }
-    uint32_t it = 0, slot = 0;
+    uint32_t slot = 0, sl = ~0u;
     const uint32_t lane_q = tid() & 3;                           // Q4_K: the lane's quarter of its super-block
-    for (uint32_t si = 0; si < n_sl; si++) {
-        const uint32_t sl = m.slice + si * m.sstep;
-        float xv[64], sx[4];
-        load_x<T>(xs, m, sl, xv, sx);
-        const bool pair_on = m.ps < m.Q && sl * m.Q + m.ps < m.n_pairs;
-        for (uint32_t k = 0; k < m.n_my; k++, it++) {
-            wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
-            uint32_t dw[M][NDW];
-            read_item<T, M>(rg.base + slot * slot_bytes(T, M), dw);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the slot is free again
-            if (it + rg.ns < n_items) {
-                dma_item<T, M>(g, m, is, rg.base);
-                advance(is, m.n_my, rg.ns);
-            }
-            if (++slot == rg.ns) slot = 0;
-            const uint32_t r = map_row(m, k);
-            const bool on = pair_on && r < m.hi;
-            float acc[M];
-#pragma unroll
-            for (int mat = 0; mat < M; mat++) {
-                acc[mat] = item_dot<T>(dw[mat], xv, sx, lane_q);
-                if (!on) acc[mat] = 0.f;
-            }
-            lane_sum<M>(acc, m.P);
-#pragma unroll
-            for (int mat = 0; mat < M; mat++)
-                if (m.ps == 0 && r < m.hi) part[((r - m.base) * M + mat) * m.S + sl] = acc[mat];
+    float xv[64], sx[4];
+    bool pair_on = false;
+    Cur cc = cur0(m);
+    for (uint32_t it = 0; it < n_items; it++) {
+        if (cc.s != sl) {                                        // a new slice: its input values
+            sl = cc.s;
+            load_x<T>(xs, m, sl, xv, sx);
+            pair_on = m.ps < m.Q && sl * m.Q + m.ps < m.n_pairs;
         }
+        wait_items<D>(it + rg.ns <= n_items ? rg.ns - 1 : 0);
+        uint32_t dw[M][NDW];
+        read_item<T, M>(rg.base + slot * slot_bytes(T, M), dw);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");      // the slot is free again
+        if (it + rg.ns < n_items) {
+            dma_item<T, M>(g, m, is, rg.base);
+            advance(is, m, rg.ns);
+        }
+        if (++slot == rg.ns) slot = 0;
+        const uint32_t r = map_row(m, cc.g);
+        const bool on = pair_on && r < m.hi;
+        float acc[M];
+#pragma unroll
+        for (int mat = 0; mat < M; mat++) {
+            acc[mat] = item_dot<T>(dw[mat], xv, sx, lane_q);
+            if (!on) acc[mat] = 0.f;
+        }
+        lane_sum<M>(acc, m.P);
+#pragma unroll
+        for (int mat = 0; mat < M; mat++)
+            if (m.ps == 0 && r < m.hi) part[((r - m.base) * M + mat) * m.S + sl] = acc[mat];
+        advance(cc, m, 1);
     }
     __syncthreads();
 }
