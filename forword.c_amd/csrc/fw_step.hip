@@ -124,31 +124,27 @@ __device__ __forceinline__ bool bar_wait(const MkArgs &a, uint32_t epoch, uint32
 
 // ── staging ──────────────────────────────────────────────────────────────────
 
-__device__ __forceinline__ float block_sum_all(float v, float *s_red)
+// RMSNorm folded into the GEMV (rms_norm, norm.c:7-16): the staged input is
+// x*w and the epilogue multiplies each row's sum by 1/sqrt(mean(x^2)+eps), so
+// no pass over the staged values waits for the sum of squares.  Each wave
+// stores its share of that sum in s_red (visible after the staging barrier);
+// norm_scale adds the eight shares in wave order.
+__device__ __forceinline__ void wave_ss(float ss, float *s_red)
 {
-    v = wave_sum(v);
-    const int lane = tid() & 63, wave = wave_id();
-    __syncthreads();
-    if (lane == 0) s_red[wave] = v;
-    __syncthreads();
+    ss = wave_sum(ss);
+    if ((tid() & 63) == 0) s_red[wave_id()] = ss;
+}
+__device__ __forceinline__ float norm_scale(const float *s_red, uint32_t n, float eps)
+{
     float r = 0.f;
 #pragma unroll
     for (int w = 0; w < MK_WAVES; w++) r += s_red[w];
-    return r;
-}
-
-// xs = (xs*w) * 1/sqrt(mean(xs^2)+eps) (rms_norm, norm.c:7-16), ss being this
-// thread's share of the sum of squares of the staged values.
-__device__ __forceinline__ void norm_staged(float *xs, uint32_t n, const float *nw, float eps, float ss, float *s_red)
-{
-    ss = block_sum_all(ss, s_red);                       // also orders every thread's staging stores
-    const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
-    const FW_GLOBAL float *w = gptr(nw);
-    for (uint32_t j = tid(); j < n; j += MK_THREADS) xs[swz(j)] = (xs[swz(j)] * w[j]) * scale;
+    return 1.0f / sqrtf((r / (float)n) + eps);
 }
 
 // xs <- src: n values published by other workgroups as {value, tag} words,
-// RMS-normalised by weights nw when given (rms_norm, norm.c:7-16).  Every
+// times the norm weights nw when given (the scale is folded into the
+// epilogue, see norm_scale; each wave's sum of squares goes to s_red).  Every
 // thread issues its loads at once and then calls issue() (this phase's first
 // weight items, which queue behind them).  Values whose tag is not yet `tag`
 // are loaded again, in batches with a back-off so early workgroups do not
@@ -200,16 +196,13 @@ __device__ __forceinline__ bool stage(const MkArgs &a, float *xs, const uint64_t
             if (j < n) {
                 const float x = __builtin_bit_cast(float, (uint32_t)v[b]);
                 ss = __builtin_fmaf(x, x, ss);
-                xs[swz(j)] = x * w[b];                             // (x * w) * scale below (norm.c order)
+                xs[swz(j)] = x * w[b];                             // (x * w), times the scale in the epilogue
             }
         }
     }
     if (!ok) *s_fail = 1;
-    if (nw) {
-        ss = block_sum_all(ss, s_red);                             // also orders the stores above
-        const float scale = 1.0f / sqrtf((ss / (float)n) + eps);
-        for (uint32_t j = t; j < n; j += MK_THREADS) xs[swz(j)] *= scale;
-    }
+    if (nw) wave_ss(ss, s_red);
+    (void)eps;
     __syncthreads();
     if (*s_fail) {
         if (t == 0) atomicOr(a.err, 1u);
@@ -772,7 +765,7 @@ __device__ __forceinline__ void wg_rows(uint32_t n_rows, uint32_t &lo, uint32_t 
 // in LDS), K/V append at pos (attention.c:129-140).  q and the new K/V row are
 // also published as words tagged `tag` for this step's attention.
 __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const float *part, const float *rope,
-                                        const float *bias, uint32_t layer, uint32_t pos, uint32_t tag)
+                                        const float *bias, uint32_t layer, uint32_t pos, uint32_t tag, float nscale)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
@@ -780,7 +773,7 @@ __device__ __forceinline__ void epi_qkv(const MkArgs &a, const MkGemv &g, const 
     const uint32_t kvd = a.n_kv * hd, nq = g.rows[0];
     for (uint32_t rl = 2 * tid(); rl < hi - lo; rl += 2 * MK_THREADS) {
         const uint32_t r = lo + rl;
-        float v0 = row_sum<1>(part, rl, 0, ns), v1 = row_sum<1>(part, rl + 1, 0, ns);
+        float v0 = row_sum<1>(part, rl, 0, ns) * nscale, v1 = row_sum<1>(part, rl + 1, 0, ns) * nscale;
         if (bias) {
             v0 += bias[r];
             v1 += bias[r + 1];
@@ -836,15 +829,16 @@ __device__ __forceinline__ float silu_f(float v)
 }
 
 // h = act(gate x) * (up x) (ffn.c:82-104): silu, or a GELU form.
-__device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part, uint32_t tag)
+__device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part, uint32_t tag,
+                                           float nscale)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
     const uint32_t ns = n_slices(g.n_cols, g.qa, g.qmin);
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
-        const float gv = row_sum<2>(part, rl, 0, ns);
+        const float gv = row_sum<2>(part, rl, 0, ns) * nscale;
         const float av = a.act == ACT_SILU ? silu_f(gv) : a.act == ACT_GELU ? gelu_erf(gv) : gelu_tanh(gv);
-        st_sys(a.hf + lo + rl, av * row_sum<2>(part, rl, 1, ns));
+        st_sys(a.hf + lo + rl, av * (row_sum<2>(part, rl, 1, ns) * nscale));
     }
     wait_mem();                                   // this wave's rows are stored
     __syncthreads();
@@ -881,7 +875,7 @@ __device__ __forceinline__ void block_best(float &bv, uint32_t &bi, float *s_v, 
 // maximum; NaN never wins; NaN at index 0 makes index 0 the answer), which also
 // advances the device-resident greedy loop (main.c:173-217).
 __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const float *part, uint32_t pos,
-                                         uint32_t greedy, uint32_t n_prompt)
+                                         uint32_t greedy, uint32_t n_prompt, float nscale)
 {
     __shared__ float s_v[MK_WAVES];
     __shared__ uint32_t s_i[MK_WAVES];
@@ -892,7 +886,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
-        const float y = row_sum<1>(part, rl, 0, ns);
+        const float y = row_sum<1>(part, rl, 0, ns) * nscale;
         st_sys(a.logits + lo + rl, y);
         if (!isnan(y) && (bi == 0xffffffffu || y > bv)) { bv = y; bi = lo + rl; }
     }
@@ -1423,11 +1417,11 @@ __device__ __forceinline__ void embed(const MkArgs &a, float *xs, float *x_own, 
         float v = a.embd_type == kF32 ? reinterpret_cast<const float *>(row)[j]
                                       : dequant_one(row + (size_t)(j / bv) * bb, a.embd_type, j % bv);
         if (a.embd_scale != 1.0f) v *= a.embd_scale;
-        xs[swz(j)] = v;
+        xs[swz(j)] = v * gptr(nw)[j];                  // (x * w), times the scale in the epilogue
         ss = __builtin_fmaf(v, v, ss);
         if (j >= lo && j < hi) x_own[j - lo] = v;
     }
-    norm_staged(xs, a.n_embd, nw, a.eps, ss, s_red);
+    wave_ss(ss, s_red);
     __syncthreads();
 }
 
@@ -1515,12 +1509,13 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                     gemv<TL, 1>(g, xs, part, lds8, lay.fixed, lay.attn, n_pre);
                 }
                 if (mixv) gemv<TMX, 1>(v_part(a, g, tab, layer), xs, part, lds8, lay.fixed, lay.attn, 0);
+                const float nscale = nw ? norm_scale(s_red, n_in, a.eps) : 1.0f;   // after gemv's barrier
                 if (kind == MK_QKV)
                     epi_qkv(a, g, part, rope,
                             a.bqkv ? a.bqkv + (size_t)layer * (a.n_embd + 2 * a.n_kv * a.head_dim) : nullptr,
-                            layer, pos, tag_out);
-                else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out);
-                else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt);
+                            layer, pos, tag_out, nscale);
+                else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out, nscale);
+                else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt, nscale);
                 else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd, tag_out);
                 n_pre = 0;
             }
