@@ -580,7 +580,7 @@ static int setup_mk(forword_gpu_t *h)
         dalloc(h, (void **)&h->d_tq, h->mk_tq_bytes, "tagged q") || dalloc(h, (void **)&h->d_tkv, h->mk_tkv_bytes, "tagged K/V row") ||
         dalloc(h, (void **)&h->d_tx, (size_t)n * 8, "tagged x") ||
         dalloc(h, (void **)&h->d_tatt, (size_t)n * 8, "tagged attention output") ||
-        dalloc(h, (void **)&h->d_hf, (size_t)c.n_ff * 4, "ffn activations") ||
+        dalloc(h, (void **)&h->d_hf, (size_t)c.n_ff * 4 * kMkStepsPerLaunch * L, "ffn activations") ||
         dalloc(h, (void **)&h->d_hflag, (size_t)wg * 128, "ffn activation flags"))
         return -1;
     if (head_q6k) {

@@ -65,8 +65,9 @@ struct MkArgs {
     // 2 * n_kv * head_dim) and the attention partials
     // [n_head][n_splits][head_dim + 2] (o, then m and l).
     uint64_t *tx, *tatt, *tq, *tkv, *tpart;
-    // The FFN activations h (n_ff floats) with one flag per workgroup (128 bytes
-    // apart) raised to the phase's epoch once its rows are stored.
+    // The FFN activations h, n_ff floats per (step of the launch, layer): slot
+    // (step * n_layer + layer), with one flag per workgroup (128 bytes apart)
+    // raised to the phase's epoch once its rows are stored.
     float *hf;
     uint32_t *hflag;
     float *trace;            // [2 * n_layer][n_embd] residual stream after each residual add

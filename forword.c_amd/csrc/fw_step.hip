@@ -213,12 +213,16 @@ __device__ __forceinline__ bool stage(const MkArgs &a, float *xs, const uint64_t
 
 // xs <- h (DOWN's input, n floats): every thread t below the workgroup count
 // waits for workgroup t's flag to reach `tag` (bounded, like a barrier wait),
-// then the workgroup loads h with 16-byte system-scope loads, up to 8 per
-// thread at once.  Half the bytes of tagged words, and one batch of loads
-// where 14336 tagged words take three.  issue() goes out first, as in stage().
+// then the workgroup loads h with 16-byte loads, up to 8 per thread at once.
+// Half the bytes of tagged words, and one batch of loads where 14336 tagged
+// words take three.  h has its own slot per (step, layer) of the launch, so
+// no cache holds a line of it before every producer has stored (caches start
+// clean at launch) and the loads may go through the L2: the first workgroup
+// of an XCD fetches each line, the other 31 hit.  issue() goes out first, as
+// in stage().
 template <typename F>
 __device__ __forceinline__ bool stage_h(const MkArgs &a, float *xs, uint32_t n, uint32_t tag, uint32_t *s_fail,
-                                        F &&issue)
+                                        F &&issue, const float *hrow)
 {
     constexpr int NB = 8;
     const uint32_t t = tid();
@@ -241,7 +245,7 @@ __device__ __forceinline__ bool stage_h(const MkArgs &a, float *xs, uint32_t n, 
         for (int b = 0; b < NB; b++) {
             const uint32_t j = j0 + 4 * (t + b * MK_THREADS);
             if (j < n)
-                asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v[b]) : "v"(gptr(a.hf) + j) : "memory");
+                asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v[b]) : "v"(gptr(hrow) + j) : "memory");
         }
         asm volatile("s_waitcnt vmcnt(0)"
                      : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
@@ -830,7 +834,7 @@ __device__ __forceinline__ float silu_f(float v)
 
 // h = act(gate x) * (up x) (ffn.c:82-104): silu, or a GELU form.
 __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, const float *part, uint32_t tag,
-                                           float nscale)
+                                           float nscale, float *hrow)
 {
     uint32_t lo, hi;
     wg_rows(g.n_rows, lo, hi);
@@ -838,7 +842,7 @@ __device__ __forceinline__ void epi_swiglu(const MkArgs &a, const MkGemv &g, con
     for (uint32_t rl = tid(); rl < hi - lo; rl += MK_THREADS) {
         const float gv = row_sum<2>(part, rl, 0, ns) * nscale;
         const float av = a.act == ACT_SILU ? silu_f(gv) : a.act == ACT_GELU ? gelu_erf(gv) : gelu_tanh(gv);
-        st_sys(a.hf + lo + rl, av * (row_sum<2>(part, rl, 1, ns) * nscale));
+        st_sys(hrow + lo + rl, av * (row_sum<2>(part, rl, 1, ns) * nscale));
     }
     wait_mem();                                   // this wave's rows are stored
     __syncthreads();
@@ -1481,6 +1485,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                                 : kind == MK_FFN ? uni(tab[layer].ffn_norm)
                                 : kind == MK_HEAD ? a.out_norm : nullptr;
                 const MkGemv g = phase_gemv(a, tab, kind, layer);
+                float *hrow = a.hf + ((size_t)step * a.n_layer + layer) * a.n_ff;   // this step's, this layer's h
                 const uint32_t mix = TM && kind != MK_HEAD ? layer_mix(tab[layer]) : 0u;
                 const bool mixd = kind == MK_DOWN && (mix & MK_MIX_DOWN), mixv = kind == MK_QKV && (mix & MK_MIX_V);
                 if (kind == MK_QKV && layer == 0) {
@@ -1495,7 +1500,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                         else n_pre = prefetch<TL, 1>(g, lds8, lay.fixed, lay.attn);
                     };
                     const bool ok = kind == MK_DOWN
-                                        ? stage_h(a, xs, n_in, epoch, &s_fail, issue)
+                                        ? stage_h(a, xs, n_in, epoch, &s_fail, issue, hrow)
                                         : stage<MK_TB_EMBD>(a, xs, src, n_in, nw, a.eps, epoch, s_red, &s_fail, issue);
                     if (!ok) return;
                 }
@@ -1514,7 +1519,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                     epi_qkv(a, g, part, rope,
                             a.bqkv ? a.bqkv + (size_t)layer * (a.n_embd + 2 * a.n_kv * a.head_dim) : nullptr,
                             layer, pos, tag_out, nscale);
-                else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out, nscale);
+                else if (kind == MK_FFN) epi_swiglu(a, g, part, tag_out, nscale, hrow);
                 else if (kind == MK_HEAD) epi_head(a, g, part, pos, greedy, n_prompt, nscale);
                 else epi_resid(a, g, part, x_own, a.trace + (size_t)(2 * layer + (kind == MK_DOWN)) * a.n_embd, tag_out);
                 n_pre = 0;
