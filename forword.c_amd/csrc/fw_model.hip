@@ -159,6 +159,10 @@ struct forword_gpu {
     MkLayer *d_layers = nullptr;
     uint64_t *d_prof = nullptr;          // phase stamps of the last launch (FORWORD_GPU_PHASE_TIMES=1)
     uint32_t prof_steps = 0;
+    // Failure injection for tests (FORWORD_GPU_ABORT_LAUNCH=k, read at init):
+    // persistent launch k (1-based) starts with the error word set, so every
+    // bounded wait in it takes its exit and forword_gpu_status reports it.
+    uint32_t mk_abort_at = 0, mk_launches = 0;
     // sampled generation (allocated on first use): probabilities, reductions, buckets,
     // history counts, PRNG state, sampled ids
     float *d_sbuf = nullptr, *d_spart = nullptr;
@@ -441,6 +445,8 @@ static int run_steps(forword_gpu_t *h, size_t n)
             MkArgs a = h->mka;
             a.epoch0 = h->mk_epoch;
             a.n_steps = k;
+            if (h->mk_abort_at && ++h->mk_launches == h->mk_abort_at)
+                HIPCHK(hipMemsetD32Async(h->d_mk_err, 1, 1, h->stream), "persistent step launch");
             HIPCHK(mk_launch(a, h->mk_tl, h->mk_th, h->mk_tm, h->mk_wg, h->mk_lds, h->stream), "persistent step launch");
             h->prof_steps = k;
             h->mk_epoch += k * mk_barriers_per_step(h->cfg.n_layer);
@@ -612,6 +618,8 @@ static int setup_mk(forword_gpu_t *h)
     a.err = h->d_mk_err;
     a.am_v = h->d_amv;
     a.am_i = h->d_ami;
+    const char *ab = getenv("FORWORD_GPU_ABORT_LAUNCH");
+    if (ab) h->mk_abort_at = (uint32_t)strtoul(ab, nullptr, 10);
     const char *pt = getenv("FORWORD_GPU_PHASE_TIMES");
     if (pt && !strcmp(pt, "1")) {
         if (dalloc(h, (void **)&h->d_prof, (1 + (size_t)kMkStepsPerLaunch * (5 * L + 1)) * 8, "phase stamps")) return -1;

@@ -162,3 +162,28 @@ def test_decode_from_after_kv_write_matches_oracle(persistent):
             assert np.array_equal(gm.decode_from(nxt, 41, 6), exp)
             gm.decode_from(nxt, 41, 3, copy_out=False)
             assert np.array_equal(gm.decode(3), exp[3:])
+
+
+def test_persistent_abort_resets_tagged_state(monkeypatch):
+    """A persistent launch that starts with the error word set (failure injected
+    from the host with FORWORD_GPU_ABORT_LAUNCH): every bounded wait in it takes
+    its exit, the call reports the failure, and the next launch, after the epoch
+    and every tagged buffer (x, q, the K/V row, the attention partials and
+    output) went back to zero, matches the oracle."""
+    monkeypatch.setenv("FORWORD_GPU_ABORT_LAUNCH", "2")
+    with fwgpu.HostModel(synth=spec_of("hd64_g4_q4")) as host, fwgpu.GpuModel(host) as gm, \
+            fw_cpu.OracleModel(host) as om:
+        assert gm.persistent
+        prompt = np.array([5, 6, 7, 8], np.uint32)
+        toks = gm.generate_greedy(prompt, 4)                           # launch 1: positions 0..6
+        pos = len(prompt) + 3
+        with pytest.raises(fwgpu.ForwordError, match="timed out"):
+            gm.decode_from(int(toks[-1]), pos, 3)                      # launch 2: aborted
+        got = gm.decode_from(int(toks[-1]), pos, 5)                    # launch 3
+        for p, t in enumerate(list(prompt) + list(toks)):
+            logits = om.forward(int(t), p)
+        exp = []
+        for p in range(pos + 1, pos + 6):
+            exp.append(fw_cpu.argmax(logits))
+            logits = om.forward(exp[-1], p)
+        assert list(got) == exp, (got, exp)
