@@ -514,7 +514,7 @@ static int setup_mk(forword_gpu_t *h)
     // a Q6_K lm-head runs from a re-laid-out copy (whole super-blocks per row required)
     const bool head_q6k = h->out.type == kQ6_K;
     const uint32_t th = head_q6k ? kQ6_KR : h->out.type;
-    if (!mk_supported(n, c.n_ff, hd, group, tl, th, h->embd.type, tm) || units + 1 > 64) return 0;
+    if (!mk_supported(n, c.n_ff, hd, group, tl, th, h->embd.type, tm) || units > 64) return 0;
     int dev = 0, cus = 0;                    // one workgroup per CU; each barrier flag is polled by one thread
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1 ||
@@ -548,6 +548,18 @@ static int setup_mk(forword_gpu_t *h)
     if (ns > 256) ns = 256;
     if (ns < 1) ns = 1;
     a.n_splits = ns;
+    // Below position 4096 half-size sub-groups: twice the units with half the
+    // heads each, so an item's scores and softmax take half as long; each K/V
+    // row is then read by two units, which costs more than it saves from a few
+    // thousand positions on (8B shape: +2 % at position 2K, -5 % at 8K, -17 %
+    // at 32K with half-size sub-groups throughout).
+    a.attn_gs_short = gs > 1 ? gs / 2 : 1;
+    a.attn_units_short = c.n_head_kv * (group / a.attn_gs_short);
+    uint32_t ns_short = (uint32_t)cus / a.attn_units_short;
+    if (ns_short > by_ctx) ns_short = by_ctx;
+    if (ns_short < 1) ns_short = 1;
+    a.n_splits_short = ns_short < ns ? ns_short : ns;
+    a.attn_long_pos = 4096;
     const size_t lds = mk_lds_bytes(a, (uint32_t)cus, tl, th, tm);
     const int wg = lds ? mk_max_workgroups(tl, th, tm, lds) : 0;
     if (wg != cus) {

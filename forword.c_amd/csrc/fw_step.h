@@ -54,6 +54,9 @@ struct MkArgs {
     // Attention units: the query heads of a KV head's group in sub-groups of
     // attn_gs (a power of two dividing the group), attn_units = n_kv * group / attn_gs.
     uint32_t attn_gs, attn_units;
+    // Below position attn_long_pos: sub-groups of attn_gs_short heads (half of
+    // attn_gs, at least 1), attn_units_short units, at most n_splits_short splits.
+    uint32_t attn_gs_short, attn_units_short, n_splits_short, attn_long_pos;
     float eps;
     float *kc, *vc;
     const float *cos_tab, *sin_tab;

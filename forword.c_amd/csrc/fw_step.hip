@@ -900,7 +900,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
         st_sys(a.am_v + blockIdx.x, bv);
         st_sys(a.am_i + blockIdx.x, bi);
         wait_mem();
-        s_last = ticket_sys(a.tickets + a.attn_units) == gridDim.x - 1;
+        s_last = ticket_sys(a.tickets) == gridDim.x - 1;
     }
     __syncthreads();
     if (!s_last) return;
@@ -921,7 +921,7 @@ __device__ __forceinline__ void epi_head(const MkArgs &a, const MkGemv &g, const
             st_sys(&a.state->token, pos + 1 < n_prompt ? a.prompt[pos + 1] : r);
             st_sys(&a.state->pos, pos + 1);
         }
-        st_sys(a.tickets + a.attn_units, 0u);
+        st_sys(a.tickets, 0u);
     }
 }
 
@@ -944,10 +944,24 @@ __device__ __forceinline__ void load_vec(const FW_GLOBAL float *p, float (&v)[EP
 // Splits of the positions 0..pos per KV head in this step: about one per 64
 // positions, at most the n_splits the partial buffer holds.  Short contexts
 // then have fewer, longer items and a cheaper combine.
+// Query-head grouping of attention at position pos: half-size sub-groups
+// (more, shorter items; each K/V row read by two units) while the K/V rows are
+// few, the full sub-group (each row read once per KV head) from
+// a.attn_long_pos on, where attention becomes bound by its K/V bytes.
+struct AttnGrp {
+    uint32_t gs, units, max_splits;
+};
+__device__ __forceinline__ AttnGrp attn_grp(const MkArgs &a, uint32_t pos)
+{
+    return pos < a.attn_long_pos ? AttnGrp{a.attn_gs_short, a.attn_units_short, a.n_splits_short}
+                                 : AttnGrp{a.attn_gs, a.attn_units, a.n_splits};
+}
+
 __device__ __forceinline__ uint32_t attn_splits_at(const MkArgs &a, uint32_t pos)
 {
     const uint32_t want = (pos + 64) / 64;
-    return want > a.n_splits ? a.n_splits : want;
+    const uint32_t cap = attn_grp(a, pos).max_splits;
+    return want > cap ? cap : want;
 }
 
 // Waits until the tagged words w[k] (k with bit k of `valid`; the others are
@@ -1003,7 +1017,7 @@ __device__ __forceinline__ bool attn_item(const MkArgs &a, uint32_t layer, uint3
 {
     constexpr uint32_t NG = 2 * MK_WAVES;                  // position streams of the workgroup
     constexpr int HD = 32 * EPL;
-    const uint32_t n_sub = a.attn_units / a.n_kv, kvh = unit / n_sub;
+    const uint32_t n_sub = attn_grp(a, pos).units / a.n_kv, kvh = unit / n_sub;
     const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * G;     // first query head of the unit
     float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
     float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
@@ -1174,7 +1188,7 @@ __device__ __forceinline__ bool attn_combine(const MkArgs &a, uint32_t unit, flo
 {
     constexpr int HD = 32 * EPL, SB = 16;
     const uint32_t ns = attn_splits_at(a, pos);
-    const uint32_t n_sub = a.attn_units / a.n_kv;
+    const uint32_t n_sub = attn_grp(a, pos).units / a.n_kv;
     const uint32_t h0 = (unit / n_sub) * (a.n_head / a.n_kv) + (unit % n_sub) * G;
     float *s_w = lds;                                      // [G][ns] m, then the split weights
     float *s_l = lds + G * ns;                             // [G][ns] l
@@ -1247,15 +1261,15 @@ template <int EPL, int G>
 __device__ __forceinline__ bool attention_t(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tin,
                                             uint32_t tag, uint32_t *s_fail)
 {
-    const uint32_t ns = attn_splits_at(a, pos), items = a.attn_units * ns;
+    const uint32_t units = attn_grp(a, pos).units, ns = attn_splits_at(a, pos), items = units * ns;
     const uint32_t per_group = ((pos + ns) / ns + 2 * MK_WAVES - 1) / (2 * MK_WAVES);   // positions per lane group
     bool ok = true;
     for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
-        const uint32_t unit = it % a.attn_units, split = it / a.attn_units;
+        const uint32_t unit = it % units, split = it / units;
         if (per_group <= 2) ok = attn_item<EPL, G, 2>(a, layer, pos, unit, split, lds, tin, tag) && ok;
         else ok = attn_item<EPL, G, EPL == 4 ? 4 : 8>(a, layer, pos, unit, split, lds, tin, tag) && ok;
     }
-    for (uint32_t unit = blockIdx.x; unit < a.attn_units; unit += gridDim.x)
+    for (uint32_t unit = blockIdx.x; unit < units; unit += gridDim.x)
         ok = attn_combine<EPL, G>(a, unit, lds, tag, pos) && ok;
     if (!ok) *s_fail = 1;
     __syncthreads();
@@ -1266,7 +1280,7 @@ template <int EPL>
 __device__ __forceinline__ bool attention_e(const MkArgs &a, uint32_t layer, uint32_t pos, float *lds, uint32_t tin,
                                             uint32_t tag, uint32_t *s_fail)
 {
-    switch (a.attn_gs) {
+    switch (attn_grp(a, pos).gs) {
     case 1: return attention_t<EPL, 1>(a, layer, pos, lds, tin, tag, s_fail);
     case 2: return attention_t<EPL, 2>(a, layer, pos, lds, tin, tag, s_fail);
     case 4: return attention_t<EPL, 4>(a, layer, pos, lds, tin, tag, s_fail);
@@ -1534,7 +1548,7 @@ __global__ __launch_bounds__(MK_THREADS) void k_decode(MkArgs a)
                 bar_arrive(a, tag_out, &s_fail);
                 if (step + 1 < a.n_steps) n_pre = prefetch<TL, 1>(phase_gemv(a, tab, MK_QKV, 0), lds8, lay.fixed, lay.attn);
                 if (!bar_wait(a, tag_out, &s_fail)) return;
-            } else if (kind == MK_QKV && blockIdx.x >= a.attn_units * attn_splits_at(a, pos)) {
+            } else if (kind == MK_QKV && blockIdx.x >= attn_grp(a, pos).units * attn_splits_at(a, pos)) {
                 n_pre = prefetch<TL, 1>(phase_gemv(a, tab, MK_WO, layer), lds8, lay.fixed, lay.attn);
             }
             epoch = tag_out;
