@@ -947,7 +947,11 @@ __device__ __forceinline__ void load_vec(const FW_GLOBAL float *p, float (&v)[EP
 // Query-head grouping of attention at position pos: half-size sub-groups
 // (more, shorter items; each K/V row read by two units) while the K/V rows are
 // few, the full sub-group (each row read once per KV head) from
-// a.attn_long_pos on, where attention becomes bound by its K/V bytes.
+// a.attn_long_pos on, where attention becomes bound by its K/V bytes.  Unit u
+// is KV head u % n_kv, sub-group u / n_kv: the items of one KV head's units
+// (item = split * units + u) are n_kv workgroups apart, on the same XCD when
+// n_kv is a multiple of 8 (workgroups go to the eight XCDs round-robin), so
+// the second unit's K/V reads can hit that XCD's L2.
 struct AttnGrp {
     uint32_t gs, units, max_splits;
 };
@@ -1017,8 +1021,8 @@ __device__ __forceinline__ bool attn_item(const MkArgs &a, uint32_t layer, uint3
 {
     constexpr uint32_t NG = 2 * MK_WAVES;                  // position streams of the workgroup
     constexpr int HD = 32 * EPL;
-    const uint32_t n_sub = attn_grp(a, pos).units / a.n_kv, kvh = unit / n_sub;
-    const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit % n_sub) * G;     // first query head of the unit
+    const uint32_t kvh = unit % a.n_kv;                    // units: (sub-group, KV head), KV head fastest
+    const uint32_t h0 = kvh * (a.n_head / a.n_kv) + (unit / a.n_kv) * G;    // first query head of the unit
     float (*s_o)[G][HD] = reinterpret_cast<float (*)[G][HD]>(lds);
     float (*s_m)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD);
     float (*s_l)[G] = reinterpret_cast<float (*)[G]>(lds + MK_WAVES * G * HD + MK_WAVES * G);
@@ -1188,8 +1192,7 @@ __device__ __forceinline__ bool attn_combine(const MkArgs &a, uint32_t unit, flo
 {
     constexpr int HD = 32 * EPL, SB = 16;
     const uint32_t ns = attn_splits_at(a, pos);
-    const uint32_t n_sub = attn_grp(a, pos).units / a.n_kv;
-    const uint32_t h0 = (unit / n_sub) * (a.n_head / a.n_kv) + (unit % n_sub) * G;
+    const uint32_t h0 = (unit % a.n_kv) * (a.n_head / a.n_kv) + (unit / a.n_kv) * G;
     float *s_w = lds;                                      // [G][ns] m, then the split weights
     float *s_l = lds + G * ns;                             // [G][ns] l
     float *s_inv = lds + 2 * G * ns;                       // [G] 1 / sum of weights
